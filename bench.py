@@ -1,0 +1,240 @@
+"""Benchmark of tilec.ext.matrix_mul on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+Prints ONE JSON line.  The headline workload is BASELINE config 2 at its
+largest size, fp32 4096^3 (the metric's "TFLOP/s + %MFMA peak at 4096^3"):
+a step is one `matrix_mul` call on resident, seeded U(-1,1) inputs; K steps
+are timed between HIP events on the stream the kernel runs on, after W
+warmup steps.  Extra objects in the same line:
+  roofline     — the 4096^3 kernel against the fp32 MFMA peak (157.3 TFLOP/s)
+  skinny       — the metric's "GB/s + %HBM roofline at M<=16" (config 1):
+                 M in {1,4,16}, K=N=4096, x2 rotated over 8 buffers (512 MiB,
+                 beyond the 256 MB Infinity Cache), launches replayed from a
+                 HIP graph so the host does not bound an 8 us kernel
+  bf16_8192    — config 4, bf16 8192^3 with fp32 accumulate, vs 2.5 PFLOP/s
+  cpu_baseline — the oracle's tiled C restatement of the reference kernel
+                 (oracle/matmul_oracle.c, OpenMP) on a bounded row sample of
+                 the same 4096^3 problem, on this box's host cores; plus
+                 torch.matmul on the CPU for the same sample
+Only one GPU: --gpus above 1 exits with a message.
+"""
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+PEAK_FP32_MFMA = 157.3   # TFLOP/s, MI355X dense fp32 matrix
+PEAK_BF16_MFMA = 2516.6  # TFLOP/s, MI355X dense bf16 matrix
+PEAK_HBM = 8000.0        # GB/s
+METRIC = "matrix_mul TFLOP/s + %MFMA peak at 4096³; GB/s + %HBM roofline at M≤16"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-extra", action="store_true", help="skip the skinny and bf16 sections")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
+    return p.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed(fn, steps, warmup, stream=None):
+    """Average ms per call of fn() over `steps` calls, between events recorded
+    on the stream the work is issued to."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = stream or torch.cuda.current_stream()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(steps):
+        fn()
+    e.record(stream)
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def kernel_name_for(M, K, N, dtype):
+    from tilec_amd import _lib, tune
+    p = tune.pick(M, K, N, dtype)
+    if p is not None:
+        return p
+    L = _lib.lib()
+    code = _lib.F32 if dtype == "f32" else _lib.BF16
+    v = L.tilec_select_variant(M, N, K, code)
+    return _lib.variants()[v]["name"], L.tilec_auto_split_k(M, N, K, code, v)
+
+
+def bench_square(args):
+    import torch
+    from oracle import oracle as O  # seeded generators only
+    from tilec_amd import ext
+    n = 4096
+    a = torch.from_numpy(O.uniform((n, n), 4)).cuda()
+    b = torch.from_numpy(O.uniform((n, n), 5)).cuda()
+    cfg = kernel_name_for(n, n, n, "f32")
+    log(f"square fp32 {n}^3 with {cfg}")
+    ms = timed(lambda: ext.matrix_mul(a, b), args.steps, args.warmup)
+    tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
+    return dict(ms=ms, tflops=tflops, config=cfg)
+
+
+def bench_skinny(steps=200):
+    """M in {1,4,16}: HBM GB/s from graph-replayed launches over rotating x2."""
+    import torch
+    from oracle import oracle as O
+    from tilec_amd import ext
+    K = N = 4096
+    nbuf = 8
+    x2s = [torch.from_numpy(O.normal((K, N), 3 + 1000 * i)).cuda() for i in range(nbuf)]
+    out = {}
+    for M in (1, 4, 16):
+        x1 = torch.from_numpy(O.normal((M, K), 2)).cuda()
+        cfg = kernel_name_for(M, K, N, "f32")
+        for i in range(nbuf):  # warm up: workspace exists before capture
+            ext.matrix_mul(x1, x2s[i])
+        torch.cuda.synchronize()
+        reps = 4 * nbuf
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            ext.matrix_mul(x1, x2s[0])
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                outs = [ext.matrix_mul(x1, x2s[i % nbuf]) for i in range(reps)]
+        torch.cuda.synchronize()
+        replays = max(1, steps // reps)
+        with torch.cuda.stream(s):
+            ms = timed(g.replay, replays, 2, stream=s) / reps
+        del outs
+        nbytes = 4 * (M * K + K * N + M * N)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"M{M}"] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, config=list(cfg))
+        log(f"skinny M={M}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({cfg})")
+    return out
+
+
+def bench_bf16(steps=10, warmup=2):
+    import torch
+    from oracle import oracle as O
+    from tilec_amd import ext
+    n = 8192
+    sigma = n ** -0.25
+    a = torch.from_numpy(O.normal((n, n), 8, std=sigma)).to(torch.bfloat16).cuda()
+    b = torch.from_numpy(O.normal((n, n), 9, std=sigma)).to(torch.bfloat16).cuda()
+    cfg = kernel_name_for(n, n, n, "bf16")
+    ms = timed(lambda: ext.matrix_mul(a, b), steps, warmup)
+    tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
+    log(f"bf16 8192^3: {ms:.3f} ms, {tflops:.1f} TFLOP/s ({cfg})")
+    return dict(ms=ms, TFLOPs=tflops, frac=tflops / PEAK_BF16_MFMA, config=list(cfg))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def bench_cpu(target_s):
+    """The oracle's tiled restatement of `_matmul_tiled` on a row sample of the
+    4096^3 problem (same seeded inputs), OpenMP over the host's cores."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    n = 4096
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    threads = min(threads, os.cpu_count() or threads)
+    O.set_num_threads(threads)
+    a = O.uniform((n, n), 4)
+    b = O.uniform((n, n), 5)
+    rows = 64
+    t = time.perf_counter()
+    O.matmul_tiled_f32(a[:rows], b)
+    t0 = time.perf_counter() - t
+    rows = int(min(n, max(64, 64 * round(target_s / max(t0, 1e-3)))))
+    rows = rows // 64 * 64
+    t = time.perf_counter()
+    O.matmul_tiled_f32(a[:rows], b)
+    dt = time.perf_counter() - t
+    tflops = 2 * rows * n * n / dt / 1e12
+    # torch.matmul on the CPU for the same sample (the reference's oracle routine)
+    torch.set_num_threads(threads)
+    ta, tb = torch.from_numpy(a[:rows]), torch.from_numpy(b)
+    ta @ tb
+    t = time.perf_counter()
+    ta @ tb
+    dtt = time.perf_counter() - t
+    log(f"cpu oracle: {rows} rows in {dt:.2f} s -> {tflops * 1e3:.1f} GFLOP/s on {threads} threads")
+    return dict(value=tflops, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"rows 0..{rows - 1} of the fp32 4096^3 product (2*{rows}*4096*4096 flop), "
+                       f"tiled BM=BN=64 BK=16 restatement of _matmul_tiled, {dt:.2f} s",
+                cpu=cpu_model(), torch_matmul_TFLOPs=2 * rows * n * n / dtt / 1e12,
+                torch_threads=torch.get_num_threads())
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "bench.py runs on one GPU only: this build has no multi-GPU path "
+                                   "(see the sharding design notes); run with --gpus 1"}), flush=True)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}), flush=True)
+        sys.exit(1)
+    from tilec_amd import _lib
+    _lib.lib()  # fail loudly if the HIP library is missing
+    props = torch.cuda.get_device_properties(0)
+
+    sq = bench_square(args)
+    extra = {}
+    if not args.no_extra:
+        extra["skinny"] = bench_skinny()
+        extra["bf16_8192"] = bench_bf16()
+    cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
+
+    rec = {
+        "metric": METRIC,
+        "value": round(sq["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sq["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded U(-1,1), generated on the CPU, resident in HBM)",
+        "config": {"workload": "BASELINE config 2 at 4096^3: fp32 square GEMM, M=N=K=4096, row-major",
+                   "M": 4096, "N": 4096, "K": 4096, "kernel": list(sq["config"])},
+        "roofline": {"bound": "mfma", "achieved": round(sq["tflops"], 3), "peak": PEAK_FP32_MFMA,
+                     "unit": "TFLOP/s", "frac": round(sq["tflops"] / PEAK_FP32_MFMA, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "device": {"name": props.name, "cus": props.multi_processor_count,
+                   "arch": getattr(props, "gcnArchName", "")},
+    }
+    rec.update(extra)
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

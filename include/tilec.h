@@ -1,0 +1,135 @@
+/*
+ * tilec.h — C ABI of libtilec_hip.so, the MI355X (gfx950) implementation of
+ * tilec's matmul op.
+ *
+ * The reference crosses its host→device boundary in one place: the launch of
+ * the tile kernel `_matmul_tiled[(cdiv(M,BM), cdiv(N,BN))](a, b, c, M, N, K,
+ * BM=, BN=, BK=)` issued by `_matrix_mul_tiled` (tilec/ext.py:54-63), which
+ * goes through `JITFunction.run` / `_launch` (tilec/jit.py:81-105) into
+ * `torch.mps.compile_shader(...)(*buffers, threads=..., group_size=...)`.
+ * Every entry point below replaces a piece of that path; the Python caller is
+ * tilec_amd/ext.py (via ctypes), which keeps the reference's public signature
+ * `matrix_mul(x1, x2)` (tilec/ext.py:66-67).
+ *
+ * Conventions shared by all entry points
+ *   - Matrices are row-major with unit column stride; ld* is the row stride in
+ *     elements (>= the row length).  After the reference's `.contiguous()`
+ *     (tilec/ext.py:59-60) ld == the number of columns.
+ *   - Outputs are float32.  Inputs are float32, or bfloat16 (fp32 accumulate).
+ *   - Nothing here allocates device memory, synchronizes, or reads the device
+ *     back: work is enqueued on `stream` (a hipStream_t; NULL = the legacy
+ *     default stream) and returns at once, like the reference's asynchronous
+ *     MPS launch (tilec/jit.py:105).
+ *   - Functions return a status code (TILEC_OK == 0).  On failure
+ *     tilec_last_error() returns a message for the calling thread.  The Python
+ *     caller maps TILEC_ERR_VALUE to ValueError (the reference's shape error,
+ *     tilec/ext.py:57-58), TILEC_ERR_TYPE to TypeError (tilec/jit.py:34-39)
+ *     and the rest to RuntimeError.
+ */
+#ifndef TILEC_H
+#define TILEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define TILEC_OK 0
+#define TILEC_ERR_VALUE 1       /* bad shape, stride, pointer or split   */
+#define TILEC_ERR_TYPE 2        /* unsupported dtype                      */
+#define TILEC_ERR_UNSUPPORTED 3 /* variant unknown or not valid for shape */
+#define TILEC_ERR_WORKSPACE 4   /* workspace missing or too small         */
+#define TILEC_ERR_HIP 5         /* HIP runtime error at launch            */
+
+/* Element types of x1 / x2 (the output is always float32). */
+#define TILEC_F32 0
+#define TILEC_BF16 1
+
+/* Kernel families (tilec_variant_info, info[0]). */
+#define TILEC_FAMILY_SKINNY 0 /* output-stationary streaming kernel, M <= 16  */
+#define TILEC_FAMILY_GEMM 1   /* LDS-staged MFMA tile GEMM                      */
+
+/* Pass as `variant` to let the library pick with its built-in rule. */
+#define TILEC_VARIANT_AUTO (-1)
+
+/*
+ * out[M,N] = x1[M,K] · x2[K,N]
+ *
+ * Replaces the launch `_matmul_tiled[grid](x1, x2, out, M, N, K, BM, BN, BK)`
+ * (tilec/ext.py:62; kernel semantics tilec/ext.py:13-24; launch
+ * tilec/jit.py:88-105).  `variant` selects a compiled kernel (see
+ * tilec_num_variants / tilec_variant_info) the way the reference's constexpr
+ * tile sizes select a compiled specialization (tilec/jit.py:66-76);
+ * `split_k` (0 = automatic) splits the reduction dimension across
+ * workgroups, the role of the legacy `split` config (tilec/ext.py:37,48-51).
+ *
+ * M == 0 or N == 0 enqueues nothing.  K == 0 writes zeros (the reference's
+ * accumulator starts at zero and its K loop runs no iterations).
+ *
+ * `workspace` must hold tilec_matmul_workspace_bytes(...) bytes (NULL/0 when
+ * that is 0).  Its first tilec_workspace_counter_bytes(...) bytes are
+ * completion counters that must be zero before the first call; every call
+ * that completes leaves them zero again, so a workspace zeroed once at
+ * allocation can be reused by later calls on the same stream.  Calls that
+ * run concurrently (different streams) need different workspaces.
+ */
+int tilec_matmul(const void* x1, const void* x2, float* out,
+                 int64_t M, int64_t N, int64_t K,
+                 int64_t ldx1, int64_t ldx2, int64_t ldo,
+                 int32_t dtype, int32_t variant, int32_t split_k,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of workspace tilec_matmul needs for these arguments (0 if none).
+ * Replaces nothing in the reference (its kernel needs no scratch); the caller
+ * allocates it the way `_matrix_mul_tiled` allocates `out` (tilec/ext.py:61).
+ */
+size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K,
+                                    int32_t dtype, int32_t variant,
+                                    int32_t split_k);
+
+/* Leading bytes of that workspace that hold the zero-initialised counters. */
+size_t tilec_workspace_counter_bytes(int64_t M, int64_t N, int64_t K,
+                                     int32_t dtype, int32_t variant,
+                                     int32_t split_k);
+
+/*
+ * The variant the library's built-in rule picks for a shape (what
+ * TILEC_VARIANT_AUTO runs), or a negative status.  The reference's
+ * equivalent is the fixed BM=BN=64, BK=16 default of `_matrix_mul_tiled`
+ * (tilec/ext.py:54); the trained per-shape choice lives host-side in
+ * tilec_amd/tune.py, as `tune.pick` does in the reference
+ * (tilec/tune.py:143-151).
+ */
+int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype);
+
+/* The split_k that split_k == 0 resolves to for this variant and shape. */
+int32_t tilec_auto_split_k(int64_t M, int64_t N, int64_t K, int32_t dtype,
+                           int32_t variant);
+
+/*
+ * Variant enumeration, for the tuner (the reference enumerates its config
+ * space in Python: `mm_configs`, tilec/ext.py:48-51).
+ *   info[0] family (TILEC_FAMILY_*)  info[1] dtype (TILEC_F32/BF16)
+ *   info[2] BM     info[3] BN        info[4] BK
+ *   info[5] waves per workgroup      info[6] max M (0 = unbounded)
+ *   info[7] unroll / pipeline depth
+ * `name` (may be NULL) receives a static string.
+ */
+int32_t tilec_num_variants(void);
+int tilec_variant_info(int32_t variant, int32_t info[8], const char** name);
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* tilec_last_error(void);
+
+/* ABI version (major * 10000 + minor * 100 + patch). */
+int32_t tilec_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILEC_H */

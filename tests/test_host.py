@@ -1,0 +1,233 @@
+"""Host logic and the C ABI, without a GPU.
+
+Covers what the reference's host code decides before it launches
+(tilec/ext.py:54-63, tilec/jit.py:34-39): shape and dtype errors, the legacy
+config-space helpers, the MI355X config space and tuner plumbing, and that
+libtilec_hip.so loads and exports every symbol include/tilec.h declares, with
+argument validation that fails before any kernel would be enqueued.
+"""
+
+import ctypes
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tilec_amd import _lib, ext, tune
+import tilec
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+# ---------------------------------------------------------------------------
+# The drop-in surface
+# ---------------------------------------------------------------------------
+
+def test_reference_names_are_available():
+    assert tilec.ext.matrix_mul is ext.matrix_mul
+    assert tilec.ext._matrix_mul_tiled is ext._matrix_mul_tiled
+    for name in ("plan", "mm_configs", "cdiv", "MAX_BLOCK", "SPLITS", "JOINS", "BLOCKS", "_blocks"):
+        assert hasattr(tilec.ext, name)
+    assert tilec.language.cdiv(5000, 4096) == 2
+    assert callable(tilec.tune.pick)
+
+
+def test_legacy_helpers_match_oracle():
+    for n in list(range(1, 300)) + [1000, 4095, 4096, 4097, 5000, 16384, 65537]:
+        assert ext.plan(n) == O.plan(n)
+        assert ext._blocks(n) == O.blocks(n)
+    for M1, N, M2 in [(129, 256, 32), (1000, 4096, 100), (8, 48, 3), (8081, 16384, 3857)]:
+        assert ext.mm_configs(M1, N, M2) == O.mm_configs(M1, N, M2)
+
+
+def test_shape_mismatch_raises_value_error():
+    with pytest.raises(ValueError, match=r"matrix_mul: shapes \(3, 4\) and \(5, 6\) don't match"):
+        ext.matrix_mul(torch.zeros(3, 4), torch.zeros(5, 6))
+
+
+def test_non_2d_raises_value_error():
+    with pytest.raises(ValueError):
+        ext.matrix_mul(torch.zeros(3), torch.zeros(3, 4))
+    with pytest.raises(ValueError):
+        ext.matrix_mul(torch.zeros(2, 3, 4), torch.zeros(4, 4))
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.float16, torch.int32])
+def test_unsupported_dtype_raises_type_error(dt):
+    with pytest.raises(TypeError):
+        ext.matrix_mul(torch.zeros(3, 4, dtype=dt), torch.zeros(4, 5, dtype=dt))
+
+
+def test_mixed_dtype_raises_type_error():
+    with pytest.raises(TypeError):
+        ext.matrix_mul(torch.zeros(3, 4), torch.zeros(4, 5, dtype=torch.bfloat16))
+
+
+def test_cpu_tensors_raise_not_fallback():
+    # No CPU fallback: host tensors are rejected, never computed on the CPU.
+    with pytest.raises(TypeError, match="ROCm GPU"):
+        ext.matrix_mul(torch.zeros(3, 4), torch.zeros(4, 5))
+
+
+# ---------------------------------------------------------------------------
+# Config space and tuner
+# ---------------------------------------------------------------------------
+
+def test_hip_configs_rules():
+    names = {v["name"]: v for v in _lib.variants()}
+    for M, K, N, dt in [(1, 4096, 4096, "f32"), (16, 4096, 4096, "f32"), (17, 4096, 4096, "f32"),
+                        (4096, 4096, 4096, "f32"), (8192, 8192, 8192, "bf16"), (3, 100, 7, "f32")]:
+        cfgs = ext.hip_configs(M, K, N, dt)
+        assert cfgs and len(cfgs) == len(set(cfgs))
+        for name, s in cfgs:
+            v = names[name]
+            assert v["dtype"] == (_lib.F32 if dt == "f32" else _lib.BF16)
+            if v["family"] == _lib.FAMILY_SKINNY:
+                assert M <= v["max_m"]
+                assert s == 1 or K // s >= 4 * v["waves"] * v["unroll"]
+            else:
+                assert s == 1
+        has_skinny = any(names[n]["family"] == _lib.FAMILY_SKINNY for n, _ in cfgs)
+        assert has_skinny == (M <= 16 and dt == "f32")
+
+
+def test_tune_features_and_shapes():
+    f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_u4", 8)
+    assert len(f) == 16 and all(math.isfinite(x) for x in f)
+    s = tune.shapes(120, seed=0)
+    assert len(s) == 120 and s == tune.shapes(120, seed=0)
+    assert any(m <= 16 for m, _, _, _ in s) and any(d == "bf16" for *_, d in s)
+
+
+def test_exported_trees_match_sklearn(tmp_path):
+    from sklearn.ensemble import GradientBoostingRegressor
+    rng = np.random.default_rng(0)
+    X = rng.normal(size=(400, 6))
+    y = np.sin(X[:, 0]) + X[:, 1] * X[:, 2] + 0.1 * rng.normal(size=400)
+    m = GradientBoostingRegressor(n_estimators=50, max_depth=3, learning_rate=0.1, random_state=0).fit(X, y)
+    path = tmp_path / "m.json"
+    tune.export(m, str(path))
+    import json
+    tm = tune.TreeModel(json.loads(path.read_text()))
+    Xt = rng.normal(size=(100, 6))
+    np.testing.assert_allclose(tm.predict(Xt), m.predict(Xt), rtol=1e-12, atol=1e-12)
+
+
+def test_pick_returns_a_valid_config_or_none():
+    for M, K, N, dt in [(16, 4096, 4096, "f32"), (4096, 4096, 4096, "f32"), (8192, 8192, 8192, "bf16")]:
+        p = tune.pick(M, K, N, dt)
+        assert p is None or p in ext.hip_configs(M, K, N, dt)
+    assert tune.pick(0, 5, 5) is None
+
+
+def test_committed_tuning_data_schema():
+    if not os.path.exists(tune.DATA):
+        pytest.skip("no MI355X tuning data committed yet")
+    rows = tune.load()
+    assert rows and set(rows[0]) == set(tune.FIELDS)
+    assert all(r["ms"] > 0 for r in rows)
+
+
+# ---------------------------------------------------------------------------
+# C ABI
+# ---------------------------------------------------------------------------
+
+def _declared_functions():
+    src = open(os.path.join(ROOT, "include", "tilec.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(tilec_\w+)\s*\(", src)))
+
+
+def test_header_declares_what_the_binding_binds():
+    declared = _declared_functions()
+    assert declared == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+
+
+def test_version_and_variants():
+    L = _lib.lib()
+    assert L.tilec_version() == 10000
+    vs = _lib.variants()
+    assert len(vs) == L.tilec_num_variants() > 0
+    assert len({v["name"] for v in vs}) == len(vs)
+    fams = {(v["family"], v["dtype"]) for v in vs}
+    assert (_lib.FAMILY_SKINNY, _lib.F32) in fams
+    assert (_lib.FAMILY_GEMM, _lib.F32) in fams and (_lib.FAMILY_GEMM, _lib.BF16) in fams
+    assert _lib.lib().tilec_variant_info(len(vs), None, None) == _lib.ERR_UNSUPPORTED
+
+
+def _call(M=8, N=8, K=8, ldx1=None, ldx2=None, ldo=None, dtype=0, variant=-1, split=0,
+          ws=None, ws_bytes=0, x1=16, x2=16, out=16):
+    # Non-null dummy pointers: every case below must fail validation before launch.
+    L = _lib.lib()
+    return L.tilec_matmul(x1, x2, out, M, N, K, ldx1 if ldx1 is not None else K,
+                          ldx2 if ldx2 is not None else N, ldo if ldo is not None else N,
+                          dtype, variant, split, ws, ws_bytes, None)
+
+
+def test_abi_rejects_bad_arguments_before_launch():
+    assert _call(dtype=7) == _lib.ERR_TYPE
+    assert _call(M=-1) == _lib.ERR_VALUE
+    assert _call(K=1 << 40) == _lib.ERR_VALUE
+    assert _call(split=-2) == _lib.ERR_VALUE
+    assert _call(ldx1=3) == _lib.ERR_VALUE
+    assert _call(ldx2=3) == _lib.ERR_VALUE
+    assert _call(ldo=3) == _lib.ERR_VALUE
+    assert _call(out=None) == _lib.ERR_VALUE
+    assert _call(x1=None) == _lib.ERR_VALUE
+    assert _call(variant=10 ** 6) == _lib.ERR_UNSUPPORTED
+    skinny = _lib.variant_id("skinny_f32_w8_u4")
+    gemm = _lib.variant_id("gemm_f32_128x128x16_w2x2")
+    bf16 = _lib.variant_id("gemm_bf16_128x128x64_w2x2")
+    assert _call(M=17, variant=skinny) == _lib.ERR_UNSUPPORTED
+    assert _call(variant=bf16, dtype=0) == _lib.ERR_UNSUPPORTED
+    assert _call(variant=gemm, split=2) == _lib.ERR_UNSUPPORTED
+    # Split K needs a workspace.
+    assert _call(M=4, N=256, K=4096, variant=skinny, split=4) == _lib.ERR_WORKSPACE
+    assert "workspace" in _lib.last_error()
+    with pytest.raises(ValueError):
+        _lib.check(_call(M=-1))
+    with pytest.raises(TypeError):
+        _lib.check(_call(dtype=9))
+    with pytest.raises(RuntimeError):
+        _lib.check(_call(variant=10 ** 6))
+
+
+def test_abi_empty_outputs_enqueue_nothing():
+    # M == 0 or N == 0: nothing to do, no device access (null pointers are fine).
+    assert _call(M=0, x1=None, x2=None, out=None) == _lib.OK
+    assert _call(N=0, x1=None, x2=None, out=None) == _lib.OK
+
+
+def test_workspace_geometry():
+    L = _lib.lib()
+    v = _lib.variant_id("skinny_f32_w8_u4")
+    assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, v, 1) == 0
+    # 64 slabs, 8 splits: 256 B of counters + 8*64*16*64 floats
+    assert L.tilec_workspace_counter_bytes(16, 4096, 4096, 0, v, 8) == 256
+    assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, v, 8) == 256 + 8 * 64 * 16 * 64 * 4
+    # splits are recomputed so that none is empty: K=10 in chunks of 4 -> 3 splits
+    assert L.tilec_matmul_workspace_bytes(1, 64, 10, 0, v, 8) == 256 + 3 * 1 * 16 * 64 * 4
+    assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, _lib.variant_id("gemm_f32_128x128x16_w2x2"), 1) == 0
+    s = L.tilec_auto_split_k(16, 4096, 4096, 0, v)
+    assert 1 <= s <= 4096 // (4 * 8 * 4)
+    assert L.tilec_auto_split_k(16, 4096, 4096, 0, _lib.variant_id("gemm_f32_128x128x16_w2x2")) == 1
+
+
+def test_select_variant_rules():
+    L = _lib.lib()
+    names = [v["name"] for v in _lib.variants()]
+    assert names[L.tilec_select_variant(1, 4096, 4096, 0)].startswith("skinny_f32")
+    assert names[L.tilec_select_variant(4096, 4096, 4096, 0)].startswith("gemm_f32")
+    assert names[L.tilec_select_variant(8192, 8192, 8192, 1)].startswith("gemm_bf16")
+    assert names[L.tilec_select_variant(4, 4096, 4096, 1)].startswith("gemm_bf16")
+    assert L.tilec_select_variant(4, 4, 4, 5) == -_lib.ERR_TYPE

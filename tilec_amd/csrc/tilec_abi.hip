@@ -1,0 +1,234 @@
+// C ABI of libtilec_hip.so (declared in include/tilec.h).
+//
+// Validates arguments the way the reference's host code does before it
+// launches (`_matrix_mul_tiled`, tilec/ext.py:55-61, and `_arg_type`,
+// tilec/jit.py:34-39), resolves the variant and split, and enqueues one
+// kernel on the caller's stream.  No allocation, no synchronization.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "common.h"
+#include "../../include/tilec.h"
+
+namespace tilec {
+const VariantDesc* skinny_variants(int* count);
+const VariantDesc* gemm_f32_variants(int* count);
+const VariantDesc* gemm_bf16_variants(int* count);
+size_t skinny_counter_bytes(int64_t N, int64_t K, int split_k);
+size_t skinny_workspace_bytes(int64_t N, int64_t K, int split_k);
+int64_t skinny_effective_splits(int64_t N, int64_t K, int split_k);
+}  // namespace tilec
+
+using namespace tilec;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+const std::vector<const VariantDesc*>& table() {
+  static std::vector<const VariantDesc*> t;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    for (auto fam : {skinny_variants, gemm_f32_variants, gemm_bf16_variants}) {
+      int n = 0;
+      const VariantDesc* v = fam(&n);
+      for (int i = 0; i < n; ++i) t.push_back(&v[i]);
+    }
+  });
+  return t;
+}
+
+int find(const char* name) {
+  const auto& t = table();
+  for (size_t i = 0; i < t.size(); ++i)
+    if (strcmp(t[i]->name, name) == 0) return (int)i;
+  return -1;
+}
+
+constexpr int64_t kMaxDim = (int64_t(1) << 31) - 1024;  // kernels index rows/cols in int32
+constexpr int kCUs = 256;                               // MI355X compute units
+
+// Built-in rule (used when the caller passes TILEC_VARIANT_AUTO).
+int auto_variant(int64_t M, int64_t N, int64_t K, int dtype) {
+  (void)K;
+  if (dtype == TILEC_F32) {
+    if (M <= 16) return find("skinny_f32_w8_u4");
+    static const char* order[] = {"gemm_f32_256x256x16_w2x2", "gemm_f32_256x128x16_w2x2",
+                                  "gemm_f32_128x128x16_w2x2", "gemm_f32_128x64x16_w2x2"};
+    for (const char* nm : order) {
+      const int v = find(nm);
+      const VariantDesc* d = table()[v];
+      if (cdiv(M, d->bm) * cdiv(N, d->bn) >= kCUs) return v;
+    }
+    return find("gemm_f32_64x64x16_w2x2");
+  }
+  static const char* order[] = {"gemm_bf16_256x256x64_w2x2", "gemm_bf16_128x128x64_w2x2"};
+  for (const char* nm : order) {
+    const int v = find(nm);
+    const VariantDesc* d = table()[v];
+    if (cdiv(M, d->bm) * cdiv(N, d->bn) >= kCUs) return v;
+  }
+  return find("gemm_bf16_64x64x64_w2x2");
+}
+
+// split_k == 0 for the streaming kernel: enough workgroups for ~2 per CU,
+// while every wave still gets at least one full unrolled batch of rows.
+int auto_split(const VariantDesc* d, int64_t N, int64_t K) {
+  if (d->family != TILEC_FAMILY_SKINNY || N <= 0 || K <= 0) return 1;
+  const int64_t slabs = cdiv(N, d->bn);
+  int64_t s = cdiv(2 * kCUs, slabs);
+  const int64_t rows_per_split_min = 4LL * d->waves * d->unroll;
+  const int64_t s_max = K / rows_per_split_min;
+  if (s > s_max) s = s_max;
+  if (s < 1) s = 1;
+  if (s > 1024) s = 1024;
+  return (int)s;
+}
+
+int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int32_t split_k,
+            const VariantDesc** out_d, int* out_split) {
+  if (dtype != TILEC_F32 && dtype != TILEC_BF16)
+    return fail(TILEC_ERR_TYPE, "tilec: unsupported dtype code %d (use float32 or bfloat16)", dtype);
+  if (M < 0 || N < 0 || K < 0 || M > kMaxDim || N > kMaxDim || K > kMaxDim)
+    return fail(TILEC_ERR_VALUE, "tilec: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                (long long)K);
+  if (split_k < 0) return fail(TILEC_ERR_VALUE, "tilec: split_k must be >= 0 (got %d)", split_k);
+  const auto& t = table();
+  int v = variant;
+  if (v == TILEC_VARIANT_AUTO) {
+    v = auto_variant(M, N, K, dtype);
+  } else if (v < 0 || v >= (int)t.size()) {
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: unknown variant %d (have %d)", v, (int)t.size());
+  }
+  const VariantDesc* d = t[v];
+  if (d->dtype != dtype)
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s is for dtype %d, not %d", d->name, d->dtype, dtype);
+  if (d->max_m > 0 && M > d->max_m)
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s takes M <= %d (got %lld)", d->name, d->max_m,
+                (long long)M);
+  int s = split_k == 0 ? auto_split(d, N, K) : split_k;
+  if (d->family != TILEC_FAMILY_SKINNY && s != 1)
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s does not split K (split_k=%d)", d->name, s);
+  if (d->family == TILEC_FAMILY_SKINNY && skinny_effective_splits(N, K, s) > 65535)
+    return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
+  *out_d = d;
+  *out_split = s;
+  return TILEC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t N, int64_t K, int64_t ldx1,
+                 int64_t ldx2, int64_t ldo, int32_t dtype, int32_t variant, int32_t split_k, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  const VariantDesc* d = nullptr;
+  int s = 1;
+  int rc = resolve(M, N, K, dtype, variant, split_k, &d, &s);
+  if (rc != TILEC_OK) return rc;
+  if (M == 0 || N == 0) return TILEC_OK;
+  if (ldo < N) return fail(TILEC_ERR_VALUE, "tilec: ldo=%lld < N=%lld", (long long)ldo, (long long)N);
+  if (out == nullptr) return fail(TILEC_ERR_VALUE, "tilec: out is NULL");
+  if (K > 0) {
+    if (x1 == nullptr || x2 == nullptr) return fail(TILEC_ERR_VALUE, "tilec: x1/x2 is NULL");
+    if (ldx1 < K) return fail(TILEC_ERR_VALUE, "tilec: ldx1=%lld < K=%lld", (long long)ldx1, (long long)K);
+    if (ldx2 < N) return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < N=%lld", (long long)ldx2, (long long)N);
+  }
+  const size_t need = d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(N, K, s) : 0;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu workspace bytes (got %zu)", d->name, need,
+                workspace == nullptr ? (size_t)0 : workspace_bytes);
+  MatmulArgs a;
+  a.x1 = x1;
+  a.x2 = x2;
+  a.out = out;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.ldx1 = ldx1 > 0 ? ldx1 : 1;
+  a.ldx2 = ldx2 > 0 ? ldx2 : 1;
+  a.ldo = ldo;
+  a.split_k = s;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = d->launch(a);
+  if (e != hipSuccess)
+    return fail(TILEC_ERR_HIP, "tilec: launching %s failed: %s", d->name, hipGetErrorString(e));
+  return TILEC_OK;
+}
+
+size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
+                                    int32_t split_k) {
+  const VariantDesc* d = nullptr;
+  int s = 1;
+  if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
+  if (M == 0 || N == 0) return 0;
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(N, K, s) : 0;
+}
+
+size_t tilec_workspace_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
+                                     int32_t split_k) {
+  const VariantDesc* d = nullptr;
+  int s = 1;
+  if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
+  if (M == 0 || N == 0) return 0;
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(N, K, s) : 0;
+}
+
+int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {
+  const VariantDesc* d = nullptr;
+  int s = 1;
+  const int rc = resolve(M, N, K, dtype, TILEC_VARIANT_AUTO, 0, &d, &s);
+  if (rc != TILEC_OK) return -rc;
+  return auto_variant(M, N, K, dtype);
+}
+
+int32_t tilec_auto_split_k(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant) {
+  const VariantDesc* d = nullptr;
+  int s = 1;
+  const int rc = resolve(M, N, K, dtype, variant, 0, &d, &s);
+  if (rc != TILEC_OK) return -rc;
+  return s;
+}
+
+int32_t tilec_num_variants(void) { return (int32_t)table().size(); }
+
+int tilec_variant_info(int32_t variant, int32_t info[8], const char** name) {
+  const auto& t = table();
+  if (variant < 0 || variant >= (int)t.size())
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: unknown variant %d", variant);
+  const VariantDesc* d = t[variant];
+  if (info) {
+    info[0] = d->family;
+    info[1] = d->dtype;
+    info[2] = d->bm;
+    info[3] = d->bn;
+    info[4] = d->bk;
+    info[5] = d->waves;
+    info[6] = d->max_m;
+    info[7] = d->unroll;
+  }
+  if (name) *name = d->name;
+  return TILEC_OK;
+}
+
+const char* tilec_last_error(void) { return g_err; }
+
+int32_t tilec_version(void) { return 10000; }
+
+}  // extern "C"

@@ -1,0 +1,226 @@
+"""tilec ops on PyTorch-ROCm tensors: `matrix_mul(x1, x2)`.
+
+Host code mirroring the reference's op module (tilec/ext.py): the same public
+call, the same shape error, the same `.contiguous()` semantics and a freshly
+allocated output, launching hand-written gfx950 kernels through the C ABI in
+libtilec_hip.so instead of a JIT-compiled Metal tile kernel.
+
+    import torch, tilec
+    x1 = torch.randn(512, 4096, device="cuda")
+    x2 = torch.randn(4096, 64, device="cuda")
+    out = tilec.ext.matrix_mul(x1, x2)
+
+Kernel choice per shape comes from `tune.pick` (the shape→config model trained
+on MI355X), falling back to the library's built-in rule when no model is
+present.  The legacy config-space helpers of the reference (`plan`,
+`mm_configs`, ...) are kept with their original meaning.
+"""
+
+import torch
+
+from . import _lib
+from .language import cdiv
+
+__all__ = [
+    "matrix_mul", "_matrix_mul_tiled", "cdiv", "plan", "mm_configs", "_blocks",
+    "MAX_BLOCK", "SPLITS", "JOINS", "BLOCKS", "hip_configs", "workspace_for",
+]
+
+# ---------------------------------------------------------------------------
+# Legacy config space of the reference's split/join/block kernel
+# (tilec/ext.py:10,29-51).  Pure integer helpers, restated with the same
+# meaning; the MI355X config space is `hip_configs` below.
+# ---------------------------------------------------------------------------
+
+MAX_BLOCK = 4096
+
+
+def plan(N, block=None):
+    """(block, chunks): the smallest power of 4 >= N capped at MAX_BLOCK, and
+    cdiv(N, block).  Restates tilec/ext.py:29-34."""
+    if block is None:
+        block = 1
+        while block < N and block < MAX_BLOCK:
+            block *= 4
+    return block, cdiv(N, block)
+
+
+SPLITS = (1, 2, 4, 8, 16, 32, 64)
+JOINS = (1, 2, 4, 8)
+BLOCKS = (256, 1024, 4096)
+
+
+def _blocks(n):
+    """Restates tilec/ext.py:43-45."""
+    top = plan(n)[0]
+    return [b for b in BLOCKS if b < top and cdiv(n, b) <= 16] + [top]
+
+
+def mm_configs(M1, N, M2):
+    """(split, join, block) triples of the legacy kernel; N is the reduction
+    dimension.  Restates tilec/ext.py:48-51."""
+    return [(p, r, b) for p in SPLITS for r in JOINS
+            if (p == 1 or N // p >= 32) and (r == 1 or M1 >= r)
+            for b in _blocks(cdiv(N, p))]
+
+
+# ---------------------------------------------------------------------------
+# MI355X config space: (variant name, split_k) pairs valid for a shape.
+# ---------------------------------------------------------------------------
+
+_SKINNY_SPLITS = (1, 2, 4, 8, 16, 32, 64)
+
+
+def hip_configs(M, K, N, dtype="f32"):
+    """Every (variant, split_k) the library can run for out[M,N] = x1[M,K]·x2[K,N].
+
+    The skinny family takes M <= 16 and a K split; the tile GEMMs take any M
+    and run unsplit.  This is the search space of tune.bench / tune.pick, as
+    `mm_configs` is for the reference's tuner (tilec/tune.py:82,148).
+    """
+    code = _dtype_code_name(dtype)
+    out = []
+    for v in _lib.variants():
+        if v["dtype"] != code or (v["max_m"] and M > v["max_m"]):
+            continue
+        if v["family"] == _lib.FAMILY_SKINNY:
+            min_rows = 4 * v["waves"] * v["unroll"]
+            for s in _SKINNY_SPLITS:
+                if s == 1 or K // s >= min_rows:
+                    out.append((v["name"], s))
+        else:
+            out.append((v["name"], 1))
+    return out
+
+
+def _dtype_code_name(dtype):
+    if dtype in ("f32", "float32", torch.float32, _lib.F32):
+        return _lib.F32
+    if dtype in ("bf16", "bfloat16", torch.bfloat16, _lib.BF16):
+        return _lib.BF16
+    raise TypeError(f"unsupported dtype {dtype!r} (use float32 or bfloat16)")
+
+
+# ---------------------------------------------------------------------------
+# Workspace: split-K partials plus completion counters.  The counters must be
+# zero before first use and every completed call leaves them zero, so one
+# zeroed buffer per (device, stream) is reused across calls.
+# ---------------------------------------------------------------------------
+
+_WORKSPACES = {}
+
+
+def workspace_for(device, stream, nbytes):
+    """A zero-initialised uint8 device buffer of at least nbytes for this stream."""
+    key = (device.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 20)
+        size = (size + (1 << 20) - 1) >> 20 << 20
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------------------
+# The op
+# ---------------------------------------------------------------------------
+
+def _operand(x, rows, cols):
+    """(tensor, row stride) usable by the kernels: unit column stride and a
+    row stride >= cols; otherwise the reference's `.contiguous()` copy
+    (tilec/ext.py:59-60)."""
+    if rows <= 1 or cols == 0:
+        if not x.is_contiguous():
+            x = x.contiguous()
+        return x, max(cols, 1)
+    if x.stride(1) == 1 and x.stride(0) >= cols:
+        return x, x.stride(0)
+    x = x.contiguous()
+    return x, max(cols, 1)
+
+
+def _prepare(x1, x2):
+    if x1.dim() != 2 or x2.dim() != 2:
+        raise ValueError(f"matrix_mul: expected 2-D tensors, got shapes {tuple(x1.shape)} "
+                         f"and {tuple(x2.shape)}")
+    M, K = x1.shape
+    K2, N = x2.shape
+    if K != K2:
+        raise ValueError(f"matrix_mul: shapes {tuple(x1.shape)} and {tuple(x2.shape)} don't match")
+    if x1.dtype != x2.dtype or x1.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"unsupported kernel arguments of dtype {x1.dtype} and {x2.dtype} "
+                        "(use float32 tensors, or bfloat16 tensors)")
+    if x1.device.type != "cuda" or x2.device != x1.device:
+        raise TypeError(f"matrix_mul needs both tensors on one ROCm GPU "
+                        f"(got {x1.device} and {x2.device})")
+    return M, K, N
+
+
+def _launch(x1, x2, M, K, N, variant, split_k):
+    dtype = _lib.F32 if x1.dtype == torch.float32 else _lib.BF16
+    a, lda = _operand(x1, M, K)
+    b, ldb = _operand(x2, K, N)
+    out = torch.empty((M, N), dtype=torch.float32, device=x1.device)
+    if M == 0 or N == 0:
+        return out
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(x1.device).cuda_stream
+    need = L.tilec_matmul_workspace_bytes(M, N, K, dtype, variant, split_k)
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        ws = workspace_for(x1.device, stream, need)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    _lib.check(L.tilec_matmul(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, lda, ldb, N,
+                              dtype, variant, split_k, ws_ptr, ws_bytes, stream))
+    return out
+
+
+def _resolve_config(config, M, K, N, dtype):
+    """config: None (tuned pick), a variant name / id, or (variant, split_k)."""
+    if config is None:
+        from . import tune
+        config = tune.pick(M, K, N, "bf16" if dtype == torch.bfloat16 else "f32")
+        if config is None:
+            return _lib.VARIANT_AUTO, 0
+    if isinstance(config, (str, int)):
+        config = (config, 0)
+    variant, split_k = config
+    if isinstance(variant, str):
+        variant = _lib.variant_id(variant)
+    return int(variant), int(split_k)
+
+
+def matrix_mul(x1, x2, config=None):
+    """out[M,N] (float32) = x1[M,K] · x2[K,N] on the GPU.
+
+    Same contract as the reference (tilec/ext.py:54-67): ValueError when K does
+    not match, strided inputs are made contiguous, the output is new.  Inputs
+    are float32, or bfloat16 (fp32 accumulate, fp32 output).  `config`
+    (optional, as the reference's tuner passes it, tilec/tune.py:37) forces a
+    (variant, split_k) from `hip_configs`.
+    """
+    M, K, N = _prepare(x1, x2)
+    variant, split_k = _resolve_config(config, M, K, N, x1.dtype)
+    return _launch(x1, x2, M, K, N, variant, split_k)
+
+
+def _matrix_mul_tiled(x1, x2, BM=64, BN=64, BK=16):
+    """Run the tile GEMM with a given output tile, as the reference's
+    `_matrix_mul_tiled(x1, x2, BM, BN, BK)` does (tilec/ext.py:54-63).
+
+    Tiles are compiled ahead of time; (BM, BN) must name one of them.  BK must
+    match too for float32; bfloat16 kernels step K by their own BK.
+    """
+    M, K, N = _prepare(x1, x2)
+    code = _lib.F32 if x1.dtype == torch.float32 else _lib.BF16
+    tiles = [v for v in _lib.variants()
+             if v["family"] == _lib.FAMILY_GEMM and v["dtype"] == code and (v["bm"], v["bn"]) == (BM, BN)]
+    exact = [v for v in tiles if v["bk"] == BK]
+    chosen = exact or (tiles if code == _lib.BF16 else [])
+    if not chosen:
+        have = sorted({(v["bm"], v["bn"], v["bk"]) for v in _lib.variants()
+                       if v["family"] == _lib.FAMILY_GEMM and v["dtype"] == code})
+        raise ValueError(f"_matrix_mul_tiled: no compiled tile BM={BM} BN={BN} BK={BK} "
+                         f"for {x1.dtype}; available (BM, BN, BK): {have}")
+    return _launch(x1, x2, M, K, N, chosen[0]["id"], 1)

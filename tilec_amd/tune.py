@@ -1,0 +1,303 @@
+"""Shape → kernel-config model for MI355X, after the reference's tuner
+(tilec/tune.py).
+
+    python -m tilec_amd.tune bench [n]   # time every config on random shapes → CSV
+    python -m tilec_amd.tune train       # fit the model, report held-out quality, export JSON
+
+Same method as the reference: benchmark every valid config of every shape
+into a resumable CSV (tilec/tune.py:68-87), fit a gradient-boosted regressor
+on log(ms) (tilec/tune.py:99-132), and let `pick` take the argmin of the
+predicted time over the configs valid for a shape (tilec/tune.py:143-151).
+What differs:
+  * the configs are the compiled gfx950 variants × split_k (`ext.hip_configs`);
+  * `machine()` queries the ROCm device instead of macOS `sysctl`;
+  * shapes include the skinny M <= 16 regime and bf16;
+  * the fitted trees are exported to JSON and evaluated here with numpy, so
+    `pick` needs neither scikit-learn nor a pickle at run time.
+"""
+
+import csv
+import json
+import math
+import os
+import random
+import sys
+from functools import lru_cache
+
+from . import _lib
+from .language import cdiv
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+DATA = os.path.join(HERE, "mm_bench_mi355x.csv")
+MODEL = os.path.join(HERE, "mm_model_mi355x.json")
+FIELDS = ["chip", "cus", "M", "K", "N", "dtype", "kernel", "BM", "BN", "BK", "split_k", "ms"]
+
+
+@lru_cache(None)
+def machine():
+    """(chip name, compute units) of GPU 0 — replaces the macOS query of
+    tilec/tune.py:19-26."""
+    import torch
+    p = torch.cuda.get_device_properties(0)
+    arch = getattr(p, "gcnArchName", "") or ""
+    return f"{p.name} {arch.split(':')[0]}".strip(), int(p.multi_processor_count)
+
+
+@lru_cache(None)
+def _variant_by_name():
+    return {v["name"]: v for v in _lib.variants()}
+
+
+def features(M, K, N, cus, dtype, kernel, split_k):
+    """Model inputs for one (shape, config); the role of tilec/tune.py:29-32.
+
+    Shape and config sizes enter as log2, plus the derived quantities that
+    decide occupancy: workgroups launched per CU and the K rows per split.
+    """
+    v = _variant_by_name()[kernel]
+    tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
+    wgs = tiles * split_k
+    lg = lambda x: math.log2(max(1, x))
+    return [lg(M), lg(K), lg(N), cus, 1.0 if dtype == "bf16" else 0.0,
+            float(v["family"]), lg(v["bm"]), lg(v["bn"]), lg(v["bk"]), float(v["waves"]),
+            float(v["unroll"]), lg(split_k), lg(tiles), math.log2(max(1, wgs) / cus),
+            lg(cdiv(K, split_k)), lg(M * K * N)]
+
+
+def time_ms(x1, x2, config, best=None, reps=5):
+    """Median of `reps` synchronized runs after one warmup, with the early
+    exit of tilec/tune.py:35-51 when a probe run is over twice the best.
+    Timed with HIP events (device time) rather than wall clock."""
+    import torch
+    from . import ext
+    ext.matrix_mul(x1, x2, config)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    ext.matrix_mul(x1, x2, config)
+    e.record()
+    e.synchronize()
+    first = s.elapsed_time(e)
+    if best is not None and first > 2 * best:
+        return first
+    times = []
+    for _ in range(reps):
+        s.record()
+        ext.matrix_mul(x1, x2, config)
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    return sorted(times)[reps // 2]
+
+
+def shapes(n=500, seed=0):
+    """Seeded random shapes (M, K, N, dtype).
+
+    Keeps the reference's log-uniform generator with its size limits
+    (tilec/tune.py:54-65; there x1 is [M1,N] and x2 is [N,M2], so its N is
+    our K) and adds the regimes MI355X serves differently: skinny M in
+    [1, 16], bf16, and ragged sizes.
+    """
+    rng = random.Random(seed)
+    out = set()
+    while len(out) < n:
+        kind = rng.random()
+        M = round(2 ** rng.uniform(7, 13))
+        K = round(2 ** rng.uniform(8, 14))
+        N = round(2 ** rng.uniform(5, 12))
+        dtype = "f32"
+        if rng.random() < 0.5:
+            K = 1 << round(math.log2(K))
+        if kind < 0.3:                      # skinny
+            M = rng.randint(1, 16)
+            N = round(2 ** rng.uniform(8, 14))
+        elif kind < 0.55:                   # bf16 tile GEMM
+            dtype = "bf16"
+        if M * K * N <= 1 << 33 and M * K <= 1 << 26 and K * N <= 1 << 26:
+            out.add((M, K, N, dtype))
+    return sorted(out, key=lambda s: s[0] * s[1] * s[2])
+
+
+def load():
+    with open(DATA) as f:
+        return [{k: (v if k in ("chip", "dtype", "kernel") else float(v)) for k, v in r.items()}
+                for r in csv.DictReader(f)]
+
+
+def bench(n=300, seed=0):
+    """Benchmark every config of `n` shapes into DATA (resumable, flushed per shape)."""
+    import torch
+    from . import ext
+    chip, cus = machine()
+    done = {(int(r["M"]), int(r["K"]), int(r["N"]), r["dtype"]) for r in load()} if os.path.exists(DATA) else set()
+    with open(DATA, "a", newline="") as f:
+        w = csv.writer(f)
+        if not done:
+            w.writerow(FIELDS)
+        g = torch.Generator().manual_seed(seed)
+        todo = shapes(n, seed)
+        for i, (M, K, N, dtype) in enumerate(todo):
+            if (M, K, N, dtype) in done:
+                continue
+            tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+            x1 = torch.randn(M, K, generator=g).to(tdt).cuda()
+            x2 = torch.randn(K, N, generator=g).to(tdt).cuda()
+            best = None
+            for kernel, split in ext.hip_configs(M, K, N, dtype):
+                v = _variant_by_name()[kernel]
+                ms = time_ms(x1, x2, (kernel, split), best)
+                best = ms if best is None else min(best, ms)
+                w.writerow([chip, cus, M, K, N, dtype, kernel, v["bm"], v["bn"], v["bk"], split, f"{ms:.6g}"])
+            f.flush()
+            print(f"{i + 1}/{len(todo)}  {M}x{K} @ {K}x{N} {dtype}  best {best:.4f} ms", flush=True)
+
+
+def row_features(r):
+    return features(int(r["M"]), int(r["K"]), int(r["N"]), r["cus"], r["dtype"], r["kernel"], int(r["split_k"]))
+
+
+def _key(r):
+    return (int(r["M"]), int(r["K"]), int(r["N"]), r["dtype"])
+
+
+def train(test_frac=0.2, seed=0, out=MODEL):
+    """Fit on log(ms), report held-out quality against the best config and the
+    library's built-in rule, refit on everything and export JSON
+    (tilec/tune.py:99-132)."""
+    from sklearn.ensemble import GradientBoostingRegressor
+    rows = load()
+    names = _variant_by_name()
+    rows = [r for r in rows if r["kernel"] in names]
+    keys = sorted({_key(r) for r in rows})
+    random.Random(seed).shuffle(keys)
+    test = set(keys[:int(len(keys) * test_frac)])
+
+    def fit(rs):
+        X = [row_features(r) for r in rs]
+        y = [math.log(max(r["ms"], 1e-6)) for r in rs]
+        return GradientBoostingRegressor(n_estimators=300, max_depth=4, learning_rate=0.05,
+                                         random_state=seed).fit(X, y)
+
+    model = fit([r for r in rows if _key(r) not in test])
+    by_shape = {}
+    for r in rows:
+        by_shape.setdefault(_key(r), []).append(r)
+    L = _lib.lib()
+    ratio_model, ratio_default = [], []
+    for k in test:
+        rs = by_shape[k]
+        best = min(r["ms"] for r in rs)
+        pred = model.predict([row_features(r) for r in rs])
+        chosen = rs[min(range(len(rs)), key=lambda i: pred[i])]
+        M, K, N, dtype = k
+        dcode = _lib.F32 if dtype == "f32" else _lib.BF16
+        auto = _lib.variants()[L.tilec_select_variant(M, N, K, dcode)]["name"]
+        auto_split = L.tilec_auto_split_k(M, N, K, dcode, _lib.variant_id(auto))
+        default = [r for r in rs if r["kernel"] == auto and int(r["split_k"]) == auto_split]
+        ratio_model.append(chosen["ms"] / best)
+        if default:
+            ratio_default.append(default[0]["ms"] / best)
+    gm = lambda v: math.exp(sum(math.log(a) for a in v) / len(v)) if v else float("nan")
+    report = {
+        "held_out_shapes": len(test),
+        "model_geomean_vs_best": gm(ratio_model),
+        "model_worst_vs_best": max(ratio_model) if ratio_model else float("nan"),
+        "builtin_geomean_vs_best": gm(ratio_default),
+        "builtin_worst_vs_best": max(ratio_default) if ratio_default else float("nan"),
+    }
+    print(f"held-out shapes: {len(test)}")
+    print(f"model   : {report['model_geomean_vs_best']:.3f}x of best (geo mean), worst {report['model_worst_vs_best']:.2f}x")
+    print(f"builtin : {report['builtin_geomean_vs_best']:.3f}x of best (geo mean), worst {report['builtin_worst_vs_best']:.2f}x")
+    model = fit(rows)
+    export(model, out, report)
+    return report
+
+
+def export(model, path, report=None):
+    """Write a fitted GradientBoostingRegressor as plain JSON trees."""
+    trees = []
+    for est in model.estimators_[:, 0]:
+        t = est.tree_
+        trees.append({
+            "left": t.children_left.tolist(), "right": t.children_right.tolist(),
+            "feature": t.feature.tolist(), "threshold": t.threshold.tolist(),
+            "value": t.value[:, 0, 0].tolist(),
+        })
+    init = float(model.init_.constant_[0][0]) if hasattr(model.init_, "constant_") else float(
+        model._raw_predict_init([[0.0] * model.n_features_in_])[0][0])
+    data = {"format": "gbr-trees-v1", "learning_rate": model.learning_rate, "init": init,
+            "n_features": int(model.n_features_in_), "trees": trees, "report": report or {}}
+    with open(path, "w") as f:
+        json.dump(data, f)
+
+
+class TreeModel:
+    """Evaluates exported trees: init + learning_rate * sum(tree(x))."""
+
+    def __init__(self, data):
+        import numpy as np
+        self.lr = data["learning_rate"]
+        self.init = data["init"]
+        self.n_features = data["n_features"]
+        self.trees = [{k: np.asarray(t[k]) for k in ("left", "right", "feature", "threshold", "value")}
+                      for t in data["trees"]]
+
+    def predict(self, X):
+        import numpy as np
+        X = np.asarray(X, dtype=np.float64)
+        out = np.full(len(X), self.init)
+        rows = np.arange(len(X))
+        for t in self.trees:
+            node = np.zeros(len(X), dtype=np.int64)
+            while True:
+                leaf = t["left"][node] < 0
+                if leaf.all():
+                    break
+                f = t["feature"][node]
+                go_left = X[rows, np.where(leaf, 0, f)] <= t["threshold"][node]
+                nxt = np.where(go_left, t["left"][node], t["right"][node])
+                node = np.where(leaf, node, nxt)
+            out += self.lr * t["value"][node]
+        return out
+
+
+@lru_cache(None)
+def _model(path=MODEL):
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return TreeModel(json.load(f))
+
+
+@lru_cache(4096)
+def pick(M, K, N, dtype="f32"):
+    """(variant name, split_k) with the least predicted time, or None to use
+    the library's built-in rule (tilec/tune.py:143-151)."""
+    model = _model()
+    if model is None or 0 in (M, K, N):
+        return None
+    from . import ext
+    cands = ext.hip_configs(M, K, N, dtype)
+    if not cands:
+        return None
+    cus = _cus()
+    pred = model.predict([features(M, K, N, cus, dtype, k, s) for k, s in cands])
+    return cands[int(pred.argmin())]
+
+
+@lru_cache(None)
+def _cus():
+    try:
+        return machine()[1]
+    except Exception:
+        return 256
+
+
+if __name__ == "__main__":
+    cmd = sys.argv[1]
+    if cmd == "bench":
+        bench(int(sys.argv[2]) if len(sys.argv) > 2 else 300)
+    elif cmd == "train":
+        train()
+    else:
+        raise SystemExit(f"usage: python -m tilec_amd.tune bench [n] | train")
