@@ -69,32 +69,37 @@ extern "C" {
  * M == 0 or N == 0 enqueues nothing.  K == 0 writes zeros (the reference's
  * accumulator starts at zero and its K loop runs no iterations).
  *
- * `workspace` must hold tilec_matmul_workspace_bytes(...) bytes (NULL/0 when
- * that is 0).  Its first tilec_workspace_counter_bytes(...) bytes are
- * completion counters that must be zero before the first call; every call
- * that completes leaves them zero again, so a workspace zeroed once at
- * allocation can be reused by later calls on the same stream.  Calls that
- * run concurrently (different streams) need different workspaces.
+ * A split K needs two device buffers (NULL/0 when their size is 0):
+ *   `workspace` — tilec_matmul_workspace_bytes(...) bytes of scratch for the
+ *                 partial sums; any contents;
+ *   `counters`  — tilec_matmul_counter_bytes(...) bytes of completion
+ *                 counters that must be zero before the call.  Every call
+ *                 that completes leaves them zero again, so a buffer zeroed
+ *                 once at allocation serves all later calls on one stream,
+ *                 whatever their shapes, as long as it is large enough.
+ * Calls that run concurrently (different streams) need their own buffers.
  */
 int tilec_matmul(const void* x1, const void* x2, float* out,
                  int64_t M, int64_t N, int64_t K,
                  int64_t ldx1, int64_t ldx2, int64_t ldo,
                  int32_t dtype, int32_t variant, int32_t split_k,
-                 void* workspace, size_t workspace_bytes, void* stream);
+                 void* workspace, size_t workspace_bytes,
+                 void* counters, size_t counter_bytes, void* stream);
 
 /*
- * Bytes of workspace tilec_matmul needs for these arguments (0 if none).
- * Replaces nothing in the reference (its kernel needs no scratch); the caller
- * allocates it the way `_matrix_mul_tiled` allocates `out` (tilec/ext.py:61).
+ * Bytes of scratch (`workspace`) tilec_matmul needs for these arguments
+ * (0 if none).  Replaces nothing in the reference (its kernel needs no
+ * scratch); the caller allocates it the way `_matrix_mul_tiled` allocates
+ * `out` (tilec/ext.py:61).
  */
 size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K,
                                     int32_t dtype, int32_t variant,
                                     int32_t split_k);
 
-/* Leading bytes of that workspace that hold the zero-initialised counters. */
-size_t tilec_workspace_counter_bytes(int64_t M, int64_t N, int64_t K,
-                                     int32_t dtype, int32_t variant,
-                                     int32_t split_k);
+/* Bytes of zero-initialised completion counters (`counters`) it needs. */
+size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K,
+                                  int32_t dtype, int32_t variant,
+                                  int32_t split_k);
 
 /*
  * The variant the library's built-in rule picks for a shape (what

@@ -88,7 +88,8 @@ def test_hip_configs_rules():
             assert v["dtype"] == (_lib.F32 if dt == "f32" else _lib.BF16)
             if v["family"] == _lib.FAMILY_SKINNY:
                 assert M <= v["max_m"]
-                assert s == 1 or K // s >= 4 * v["waves"] * v["unroll"]
+                eff = ext._skinny_splits(K, s, v["bk"])
+                assert eff == 1 or K // eff >= 16 * v["waves"]
             else:
                 assert s == 1
         has_skinny = any(names[n]["family"] == _lib.FAMILY_SKINNY for n, _ in cfgs)
@@ -96,7 +97,7 @@ def test_hip_configs_rules():
 
 
 def test_tune_features_and_shapes():
-    f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_u4", 8)
+    f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8)
     assert len(f) == 16 and all(math.isfinite(x) for x in f)
     s = tune.shapes(120, seed=0)
     assert len(s) == 120 and s == tune.shapes(120, seed=0)
@@ -166,12 +167,12 @@ def test_version_and_variants():
 
 
 def _call(M=8, N=8, K=8, ldx1=None, ldx2=None, ldo=None, dtype=0, variant=-1, split=0,
-          ws=None, ws_bytes=0, x1=16, x2=16, out=16):
+          ws=None, ws_bytes=0, cnt=None, cnt_bytes=0, x1=16, x2=16, out=16):
     # Non-null dummy pointers: every case below must fail validation before launch.
     L = _lib.lib()
     return L.tilec_matmul(x1, x2, out, M, N, K, ldx1 if ldx1 is not None else K,
                           ldx2 if ldx2 is not None else N, ldo if ldo is not None else N,
-                          dtype, variant, split, ws, ws_bytes, None)
+                          dtype, variant, split, ws, ws_bytes, cnt, cnt_bytes, None)
 
 
 def test_abi_rejects_bad_arguments_before_launch():
@@ -185,7 +186,7 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert _call(out=None) == _lib.ERR_VALUE
     assert _call(x1=None) == _lib.ERR_VALUE
     assert _call(variant=10 ** 6) == _lib.ERR_UNSUPPORTED
-    skinny = _lib.variant_id("skinny_f32_w8_u4")
+    skinny = _lib.variant_id("skinny_f32_w8_b1")
     gemm = _lib.variant_id("gemm_f32_128x128x16_w2x2")
     bf16 = _lib.variant_id("gemm_bf16_128x128x64_w2x2")
     assert _call(M=17, variant=skinny) == _lib.ERR_UNSUPPORTED
@@ -194,6 +195,9 @@ def test_abi_rejects_bad_arguments_before_launch():
     # Split K needs a workspace.
     assert _call(M=4, N=256, K=4096, variant=skinny, split=4) == _lib.ERR_WORKSPACE
     assert "workspace" in _lib.last_error()
+    # ... and zeroed counters
+    assert _call(M=4, N=256, K=4096, variant=skinny, split=4, ws=16, ws_bytes=1 << 30) == _lib.ERR_WORKSPACE
+    assert "counters" in _lib.last_error()
     with pytest.raises(ValueError):
         _lib.check(_call(M=-1))
     with pytest.raises(TypeError):
@@ -210,13 +214,23 @@ def test_abi_empty_outputs_enqueue_nothing():
 
 def test_workspace_geometry():
     L = _lib.lib()
-    v = _lib.variant_id("skinny_f32_w8_u4")
-    assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, v, 1) == 0
-    # 64 slabs, 8 splits: 256 B of counters + 8*64*16*64 floats
-    assert L.tilec_workspace_counter_bytes(16, 4096, 4096, 0, v, 8) == 256
-    assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, v, 8) == 256 + 8 * 64 * 16 * 64 * 4
-    # splits are recomputed so that none is empty: K=10 in chunks of 4 -> 3 splits
-    assert L.tilec_matmul_workspace_bytes(1, 64, 10, 0, v, 8) == 256 + 3 * 1 * 16 * 64 * 4
+    v = _lib.variant_id("skinny_f32_w8_b1")
+    part = 16 * 64 * 4  # partial sums per split and 64-column slab
+    assert L.tilec_matmul_workspace_bytes(16, 1000, 1000, 0, v, 1) == 0
+    assert L.tilec_matmul_counter_bytes(16, 1000, 1000, 0, v, 1) == 0
+    # a workgroup takes at most 1024 rows of K: K=4096 runs at least 4 splits
+    assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, v, 1) == 4 * 64 * part
+    # 64 slabs, 8 splits; one counter per slab, each on its own 256-byte line
+    assert L.tilec_matmul_counter_bytes(16, 4096, 4096, 0, v, 8) == 64 * 256
+    assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, v, 8) == 8 * 64 * part
+    # splits are recomputed so that none is empty: K=100 in 16-row chunks -> 7 splits
+    assert L.tilec_matmul_workspace_bytes(1, 64, 100, 0, v, 8) == 7 * part
+    assert L.tilec_matmul_workspace_bytes(1, 64, 10, 0, v, 8) == 0  # one 16-row chunk
+    # Python's view of the split rule agrees with the library's
+    for K, s in [(4096, 1), (4096, 8), (100, 8), (10, 8), (5000, 3), (65536, 2)]:
+        nbytes = L.tilec_matmul_workspace_bytes(1, 64, K, 0, v, s)
+        eff = ext._skinny_splits(K, s, 1024)
+        assert nbytes == (0 if eff == 1 else eff * part), (K, s)
     assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, _lib.variant_id("gemm_f32_128x128x16_w2x2"), 1) == 0
     s = L.tilec_auto_split_k(16, 4096, 4096, 0, v)
     assert 1 <= s <= 4096 // (4 * 8 * 4)

@@ -295,15 +295,21 @@ def test_workspace_counters_return_to_zero():
     da, db = dev(a), dev(b)
     ref = O.matmul_f64(a, b)
     L = _lib.lib()
-    for cfg in [("skinny_f32_w8_u4", 8), ("skinny_f32_w4_u8", 16), ("skinny_f32_w16_u4", 4)]:
+    for cfg in [("skinny_f32_w8_b1", 8), ("skinny_f32_w4_b2", 16), ("skinny_f32_w16_b1", 4), ("skinny_f32_w8_b2", 64)]:
         for _ in range(3):
             got = run(da, db, cfg)
             assert O.rel_l2(got, ref) <= O.TOL_F32, cfg
         v = _lib.variant_id(cfg[0])
-        cb = L.tilec_workspace_counter_bytes(16, 4096, 4096, 0, v, cfg[1])
+        cb = L.tilec_matmul_counter_bytes(16, 4096, 4096, 0, v, cfg[1])
         stream = torch.cuda.current_stream().cuda_stream
-        ws = ext._WORKSPACES[(da.device.index, stream)]
-        assert torch.count_nonzero(ws[:cb]).item() == 0, cfg
+        cnt = ext._COUNTERS[(da.device.index, stream)]
+        assert cb > 0 and torch.count_nonzero(cnt).item() == 0, cfg
+    # calls of different shapes share the buffers: layouts must not collide
+    for m, k, n in [(1, 4096, 130), (16, 4096, 4096), (3, 4000, 65), (16, 65536, 64), (2, 4096, 130)]:
+        a1, b1 = O.normal((m, k), m + k), O.normal((k, n), n)
+        for cfg in ext.hip_configs(m, k, n, "f32"):
+            if cfg[0].startswith("skinny"):
+                assert O.rel_l2(run(dev(a1), dev(b1), cfg), O.matmul_f64(a1, b1)) <= O.TOL_F32, (cfg, (m, k, n))
     say("workspace counters ok")
 
 
@@ -326,7 +332,7 @@ def test_graph_capture_replays():
     # with eager work between replays; every replay must match eager.
     a, b = O.normal((16, 4096), 24), O.normal((4096, 2048), 25)
     da, db = dev(a), dev(b)
-    eager = ext.matrix_mul(da, db, ("skinny_f32_w8_u4", 8))
+    eager = ext.matrix_mul(da, db, ("skinny_f32_w8_b1", 8))
     eager2 = ext.matrix_mul(da, db)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -334,11 +340,11 @@ def test_graph_capture_replays():
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         # the workspace for this stream is allocated (and zeroed) before capture
-        ext.matrix_mul(da, db, ("skinny_f32_w8_u4", 8))
+        ext.matrix_mul(da, db, ("skinny_f32_w8_b1", 8))
         ext.matrix_mul(da, db)
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=s):
-            out = ext.matrix_mul(da, db, ("skinny_f32_w8_u4", 8))
+            out = ext.matrix_mul(da, db, ("skinny_f32_w8_b1", 8))
             out2 = ext.matrix_mul(da, db)
     torch.cuda.current_stream().wait_stream(s)
     for i in range(4):

@@ -24,9 +24,9 @@ VARIANT_AUTO = -1
 _i64, _i32, _vp, _sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t
 SIGNATURES = {
     "tilec_matmul": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
-                                    _i32, _i32, _i32, _vp, _sz, _vp]),
+                                    _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp]),
     "tilec_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
-    "tilec_workspace_counter_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
+    "tilec_matmul_counter_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
     "tilec_select_variant": (_i32, [_i64, _i64, _i64, _i32]),
     "tilec_auto_split_k": (_i32, [_i64, _i64, _i64, _i32, _i32]),
     "tilec_num_variants": (_i32, []),

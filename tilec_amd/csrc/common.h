@@ -24,8 +24,10 @@ struct MatmulArgs {
   int64_t M, N, K;
   int64_t ldx1, ldx2, ldo;
   int split_k;           // resolved (>= 1)
-  void* workspace;       // counters first, then partials
+  void* workspace;       // split-K partial sums (scratch)
   size_t workspace_bytes;
+  unsigned* counters;    // zero-initialised completion counters, left zero
+  size_t counter_bytes;
   hipStream_t stream;
 };
 
@@ -63,6 +65,34 @@ __device__ __forceinline__ f32x16 mfma32x32x16bf16(bf16x8 a, bf16x8 b, f32x16 c)
 }
 __device__ __forceinline__ f32x4 mfma16x16x32bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Raw buffer loads.  A load whose byte offset is >= the resource's
+// num_records returns zeros without touching memory; kernels pass kOob as the
+// offset of a masked element instead of selecting on the loaded value.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+constexpr uint32_t kOob = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
+
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t num_records = 0x7FFFFFFFu) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_records, kRsrcWord3);
+}
+__device__ __forceinline__ float load_f32(BufRsrc r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ f32x4 load_f32x4(BufRsrc r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+// Agent-coherent (sc1) accesses: the cache policy of agent-scope atomic loads
+// and stores, for data that workgroups on different XCDs exchange.
+constexpr int kCpolSc1 = 16;
+__device__ __forceinline__ f32x4 load_f32x4_coherent(BufRsrc r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCpolSc1));
+}
+__device__ __forceinline__ void store_f32x4_coherent(BufRsrc r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, (int)off, 0, kCpolSc1);
 }
 
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

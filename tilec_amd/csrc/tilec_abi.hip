@@ -60,11 +60,20 @@ int find(const char* name) {
 constexpr int64_t kMaxDim = (int64_t(1) << 31) - 1024;  // kernels index rows/cols in int32
 constexpr int kCUs = 256;                               // MI355X compute units
 
+// The skinny kernel addresses x2 within one 16-row block with 32-bit byte
+// offsets (row * ldx2 * 4, row < 16, must stay < 2^31), and its split-K
+// partials with 32-bit offsets (splits * slabs * 4 KiB < 2^31).
+constexpr int64_t kSkinnyMaxLdx1 = int64_t(1) << 25;
+constexpr int64_t kSkinnyMaxLdx2 = int64_t(1) << 25;
+constexpr int64_t kSkinnyMaxPartials = int64_t(1) << 19;  // splits * slabs
+
+bool skinny_fits(int64_t ldx1, int64_t ldx2) { return ldx1 < kSkinnyMaxLdx1 && ldx2 < kSkinnyMaxLdx2; }
+
 // Built-in rule (used when the caller passes TILEC_VARIANT_AUTO).
-int auto_variant(int64_t M, int64_t N, int64_t K, int dtype) {
+int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2) {
   (void)K;
   if (dtype == TILEC_F32) {
-    if (M <= 16) return find("skinny_f32_w8_u4");
+    if (M <= 16 && skinny_fits(ldx1, ldx2)) return find("skinny_f32_w8_b1");
     static const char* order[] = {"gemm_f32_256x256x16_w2x2", "gemm_f32_256x128x16_w2x2",
                                   "gemm_f32_128x128x16_w2x2", "gemm_f32_128x64x16_w2x2"};
     for (const char* nm : order) {
@@ -89,7 +98,7 @@ int auto_split(const VariantDesc* d, int64_t N, int64_t K) {
   if (d->family != TILEC_FAMILY_SKINNY || N <= 0 || K <= 0) return 1;
   const int64_t slabs = cdiv(N, d->bn);
   int64_t s = cdiv(2 * kCUs, slabs);
-  const int64_t rows_per_split_min = 4LL * d->waves * d->unroll;
+  const int64_t rows_per_split_min = 16LL * d->waves;  // one 16-row block per wave
   const int64_t s_max = K / rows_per_split_min;
   if (s > s_max) s = s_max;
   if (s < 1) s = 1;
@@ -97,8 +106,9 @@ int auto_split(const VariantDesc* d, int64_t N, int64_t K) {
   return (int)s;
 }
 
+// ldx1 / ldx2 <= 0 mean "contiguous" (K and N).
 int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int32_t split_k,
-            const VariantDesc** out_d, int* out_split) {
+            const VariantDesc** out_d, int* out_split, int64_t ldx1 = 0, int64_t ldx2 = 0) {
   if (dtype != TILEC_F32 && dtype != TILEC_BF16)
     return fail(TILEC_ERR_TYPE, "tilec: unsupported dtype code %d (use float32 or bfloat16)", dtype);
   if (M < 0 || N < 0 || K < 0 || M > kMaxDim || N > kMaxDim || K > kMaxDim)
@@ -108,7 +118,7 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
   const auto& t = table();
   int v = variant;
   if (v == TILEC_VARIANT_AUTO) {
-    v = auto_variant(M, N, K, dtype);
+    v = auto_variant(M, N, K, dtype, ldx1 > 0 ? ldx1 : K, ldx2 > 0 ? ldx2 : N);
   } else if (v < 0 || v >= (int)t.size()) {
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: unknown variant %d (have %d)", v, (int)t.size());
   }
@@ -118,11 +128,19 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
   if (d->max_m > 0 && M > d->max_m)
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s takes M <= %d (got %lld)", d->name, d->max_m,
                 (long long)M);
+  if (d->family == TILEC_FAMILY_SKINNY && !skinny_fits(ldx1 > 0 ? ldx1 : K, ldx2 > 0 ? ldx2 : N))
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s needs ldx1 < 2^25 and ldx2 < 2^25", d->name);
   int s = split_k == 0 ? auto_split(d, N, K) : split_k;
   if (d->family != TILEC_FAMILY_SKINNY && s != 1)
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s does not split K (split_k=%d)", d->name, s);
-  if (d->family == TILEC_FAMILY_SKINNY && skinny_effective_splits(N, K, s) > 65535)
-    return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
+  if (d->family == TILEC_FAMILY_SKINNY) {
+    const int64_t splits = skinny_effective_splits(N, K, s);
+    if (splits > 65535)
+      return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
+    if (splits > 1 && splits * cdiv(N, d->bn) >= kSkinnyMaxPartials)
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits x %lld slabs of partials is too many",
+                  d->name, (long long)splits, (long long)cdiv(N, d->bn));
+  }
   *out_d = d;
   *out_split = s;
   return TILEC_OK;
@@ -134,11 +152,11 @@ extern "C" {
 
 int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t N, int64_t K, int64_t ldx1,
                  int64_t ldx2, int64_t ldo, int32_t dtype, int32_t variant, int32_t split_k, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+                 size_t workspace_bytes, void* counters, size_t counter_bytes, void* stream) {
   g_err[0] = 0;
   const VariantDesc* d = nullptr;
   int s = 1;
-  int rc = resolve(M, N, K, dtype, variant, split_k, &d, &s);
+  int rc = resolve(M, N, K, dtype, variant, split_k, &d, &s, ldx1, ldx2);
   if (rc != TILEC_OK) return rc;
   if (M == 0 || N == 0) return TILEC_OK;
   if (ldo < N) return fail(TILEC_ERR_VALUE, "tilec: ldo=%lld < N=%lld", (long long)ldo, (long long)N);
@@ -148,10 +166,15 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
     if (ldx1 < K) return fail(TILEC_ERR_VALUE, "tilec: ldx1=%lld < K=%lld", (long long)ldx1, (long long)K);
     if (ldx2 < N) return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < N=%lld", (long long)ldx2, (long long)N);
   }
-  const size_t need = d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(N, K, s) : 0;
+  const bool skinny = d->family == TILEC_FAMILY_SKINNY;
+  const size_t need = skinny ? skinny_workspace_bytes(N, K, s) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu workspace bytes (got %zu)", d->name, need,
                 workspace == nullptr ? (size_t)0 : workspace_bytes);
+  const size_t need_cnt = skinny ? skinny_counter_bytes(N, K, s) : 0;
+  if (need_cnt > 0 && (counters == nullptr || counter_bytes < need_cnt))
+    return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu bytes of counters (got %zu)", d->name, need_cnt,
+                counters == nullptr ? (size_t)0 : counter_bytes);
   MatmulArgs a;
   a.x1 = x1;
   a.x2 = x2;
@@ -165,6 +188,8 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
   a.split_k = s;
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
+  a.counters = static_cast<unsigned*>(counters);
+  a.counter_bytes = counter_bytes;
   a.stream = static_cast<hipStream_t>(stream);
   const hipError_t e = d->launch(a);
   if (e != hipSuccess)
@@ -181,8 +206,8 @@ size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t dty
   return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(N, K, s) : 0;
 }
 
-size_t tilec_workspace_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
-                                     int32_t split_k) {
+size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
+                                  int32_t split_k) {
   const VariantDesc* d = nullptr;
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
@@ -195,7 +220,7 @@ int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {
   int s = 1;
   const int rc = resolve(M, N, K, dtype, TILEC_VARIANT_AUTO, 0, &d, &s);
   if (rc != TILEC_OK) return -rc;
-  return auto_variant(M, N, K, dtype);
+  return auto_variant(M, N, K, dtype, K, N);
 }
 
 int32_t tilec_auto_split_k(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant) {

@@ -23,7 +23,7 @@ from .language import cdiv
 
 __all__ = [
     "matrix_mul", "_matrix_mul_tiled", "cdiv", "plan", "mm_configs", "_blocks",
-    "MAX_BLOCK", "SPLITS", "JOINS", "BLOCKS", "hip_configs", "workspace_for",
+    "MAX_BLOCK", "SPLITS", "JOINS", "BLOCKS", "hip_configs", "workspace_for", "counters_for",
 ]
 
 # ---------------------------------------------------------------------------
@@ -84,13 +84,28 @@ def hip_configs(M, K, N, dtype="f32"):
         if v["dtype"] != code or (v["max_m"] and M > v["max_m"]):
             continue
         if v["family"] == _lib.FAMILY_SKINNY:
-            min_rows = 4 * v["waves"] * v["unroll"]
+            # A workgroup takes at most BK rows of K (its x1 chunk lives in
+            # LDS), so small splits are raised; keep one entry per distinct
+            # effective split, each giving every wave at least one 16-row block.
+            seen = set()
             for s in _SKINNY_SPLITS:
-                if s == 1 or K // s >= min_rows:
-                    out.append((v["name"], s))
+                eff = _skinny_splits(K, s, v["bk"])
+                if eff in seen or (eff > 1 and K // eff < 16 * v["waves"]):
+                    continue
+                seen.add(eff)
+                out.append((v["name"], s))
         else:
             out.append((v["name"], 1))
     return out
+
+
+def _skinny_splits(K, split_k, kc_max):
+    """Splits the skinny kernel actually runs (tilec_amd/csrc/skinny.hip, skinny_geom)."""
+    if K <= 0:
+        return 1
+    s = max(split_k, 1, cdiv(K, kc_max))
+    kc = cdiv(cdiv(K, s), 16) * 16
+    return cdiv(K, kc)
 
 
 def _dtype_code_name(dtype):
@@ -102,24 +117,37 @@ def _dtype_code_name(dtype):
 
 
 # ---------------------------------------------------------------------------
-# Workspace: split-K partials plus completion counters.  The counters must be
-# zero before first use and every completed call leaves them zero, so one
-# zeroed buffer per (device, stream) is reused across calls.
+# Split-K buffers, one pair per (device, stream): scratch for the partial sums
+# (any contents) and completion counters, zeroed once at allocation; every
+# completed call leaves the counters zero, so both are reused across calls of
+# any shape.  A buffer is only replaced (by a larger one) when a call needs
+# more; code that captures calls into a HIP graph runs them once before
+# capture so the buffers the graph records stay in place.
 # ---------------------------------------------------------------------------
 
-_WORKSPACES = {}
+_SCRATCH = {}
+_COUNTERS = {}
+
+
+def _buffer(table, device, stream, nbytes, zero, quantum):
+    key = (device.index, stream)
+    buf = table.get(key)
+    if buf is None or buf.numel() < nbytes:
+        size = max(nbytes, quantum)
+        size = (size + quantum - 1) // quantum * quantum
+        buf = (torch.zeros if zero else torch.empty)(size, dtype=torch.uint8, device=device)
+        table[key] = buf
+    return buf
 
 
 def workspace_for(device, stream, nbytes):
-    """A zero-initialised uint8 device buffer of at least nbytes for this stream."""
-    key = (device.index, stream)
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        size = max(nbytes, 1 << 20)
-        size = (size + (1 << 20) - 1) >> 20 << 20
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = ws
-    return ws
+    """Scratch (uint8 device tensor, >= nbytes) for split-K partial sums."""
+    return _buffer(_SCRATCH, device, stream, nbytes, False, 1 << 20)
+
+
+def counters_for(device, stream, nbytes):
+    """Zero-initialised completion counters (uint8 device tensor, >= nbytes)."""
+    return _buffer(_COUNTERS, device, stream, nbytes, True, 1 << 16)
 
 
 # ---------------------------------------------------------------------------
@@ -166,13 +194,15 @@ def _launch(x1, x2, M, K, N, variant, split_k):
         return out
     L = _lib.lib()
     stream = torch.cuda.current_stream(x1.device).cuda_stream
+    ws_ptr, ws_bytes, cnt_ptr, cnt_bytes = None, 0, None, 0
     need = L.tilec_matmul_workspace_bytes(M, N, K, dtype, variant, split_k)
-    ws_ptr, ws_bytes = None, 0
     if need:
         ws = workspace_for(x1.device, stream, need)
         ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+        cnt = counters_for(x1.device, stream, L.tilec_matmul_counter_bytes(M, N, K, dtype, variant, split_k))
+        cnt_ptr, cnt_bytes = cnt.data_ptr(), cnt.numel()
     _lib.check(L.tilec_matmul(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, lda, ldb, N,
-                              dtype, variant, split_k, ws_ptr, ws_bytes, stream))
+                              dtype, variant, split_k, ws_ptr, ws_bytes, cnt_ptr, cnt_bytes, stream))
     return out
 
 
