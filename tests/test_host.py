@@ -188,7 +188,7 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert _call(variant=10 ** 6) == _lib.ERR_UNSUPPORTED
     skinny = _lib.variant_id("skinny_f32_w8_b1")
     gemm = _lib.variant_id("gemm_f32_128x128x16_w2x2")
-    bf16 = _lib.variant_id("gemm_bf16_128x128x64_w2x2")
+    bf16 = _lib.variant_id("gemm_bf16_128x128x64_r4")
     assert _call(M=17, variant=skinny) == _lib.ERR_UNSUPPORTED
     assert _call(variant=bf16, dtype=0) == _lib.ERR_UNSUPPORTED
     assert _call(variant=gemm, split=2) == _lib.ERR_UNSUPPORTED

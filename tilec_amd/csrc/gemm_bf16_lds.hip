@@ -5,12 +5,17 @@
 // (tilec/ext.py:13-24): zero accumulator, K steps over masked tiles with
 // `other=0.0`, masked store.  Built for gfx950:
 //   * Global -> LDS with buffer_load_dwordx4 ... lds: each lane moves 16 bytes
-//     straight into LDS, no VGPR staging, asynchronously; the next K step's
-//     tiles are in flight while the current one is multiplied (two LDS
-//     buffers, one barrier per K step).
-//   * A lives in LDS row-major (k contiguous, 128-byte rows) with the 16-byte
-//     chunks of row i XOR-swizzled by (i >> 1) & 7, so the 16-byte operand
-//     reads of 16 consecutive rows hit distinct banks.
+//     straight into LDS, asynchronously, with no VGPR staging.  K steps of BK
+//     cycle through a ring of NBUF stage buffers: the loads of step k+NBUF-1
+//     are issued while step k is multiplied, so NBUF-1 steps (up to 96 KiB
+//     per CU) are in flight — the global->LDS stream, not the matrix cores,
+//     is what a shallower pipeline is limited by.
+//   * The stage buffers are distinct LDS objects and the K loop is unrolled
+//     over the ring, so every access names its buffer statically and the
+//     compiler knows reads of one buffer do not wait on loads into another.
+//   * A lives in LDS row-major (k contiguous) with its 16-byte chunks
+//     XOR-swizzled per row, so the 16-byte operand reads of 16 consecutive
+//     rows hit distinct banks.
 //   * B lives in LDS as it is in memory (n contiguous) and the MFMA B operand
 //     (8 consecutive k of one column per lane) comes from two
 //     ds_read_b64_tr_b16 transposing reads; chunks of row k are swizzled by
@@ -29,41 +34,65 @@ namespace {
 
 typedef unsigned short u16;
 typedef short i16x4v __attribute__((ext_vector_type(4)));
+typedef short i16x8v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int kBK = 64;
-
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int BK, int NBUF, int WM, int WN>
 struct LdsGemm {
   static constexpr int NW = WM * WN;
   static constexpr int NT = NW * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int A_CHUNKS = BM * kBK / 8;  // 16-byte chunks per stage
-  static constexpr int B_CHUNKS = kBK * BN / 8;
-  static constexpr int A_INSTR = A_CHUNKS / 64 / NW;  // DMA instructions per wave per stage
+  static constexpr int A_ROW_CHUNKS = BK / 8;  // 16-byte chunks per A row
+  static constexpr int B_ROW_CHUNKS = BN / 8;  // 16-byte chunks per B row
+  static constexpr int A_CHUNKS = BM * A_ROW_CHUNKS;
+  static constexpr int B_CHUNKS = BK * B_ROW_CHUNKS;
+  static constexpr int A_INSTR = A_CHUNKS / 64 / NW;  // DMA instructions per wave per step
   static constexpr int B_INSTR = B_CHUNKS / 64 / NW;
-  static constexpr int B_ROW_CHUNKS = BN / 8;
-  static constexpr int A_BYTES = BM * kBK * 2, B_BYTES = kBK * BN * 2;
+  static constexpr int IPS = A_INSTR + B_INSTR;
+  static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
   static_assert(A_CHUNKS % (64 * NW) == 0 && B_CHUNKS % (64 * NW) == 0, "DMA must divide evenly");
   static_assert(BN % 128 == 0, "B swizzle needs rows of >= 16 chunks");
+  static_assert(BK == 32 || BK == 64, "A swizzle covers 4 or 8 chunks per row");
+  static_assert(NBUF >= 2 && NBUF <= 4, "ring of 2..4 stage buffers");
+  static_assert((size_t)NBUF * STAGE_BYTES <= 160 * 1024, "LDS is 160 KiB");
+  static_assert((NBUF - 2) * IPS <= 63, "vmcnt is 6 bits");
 };
 
-__device__ __forceinline__ int swz_a(int row) { return (row >> 1) & 7; }
+// A: chunk c of row i is stored at (c ^ swz) within the row; BK=64 rows are
+// 128 B (8 chunks, 2 rows per 256-byte bank line), BK=32 rows 64 B (4 chunks).
+template <int BK>
+__device__ __forceinline__ int swz_a(int row) {
+  return BK == 64 ? (row >> 1) & 7 : (row >> 2) & 3;
+}
 __device__ __forceinline__ int swz_b(int krow) { return 4 * (krow & 3); }
 
-template <int BM, int BN, int WM, int WN>
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left unconstrained (gfx9
+// encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int BK, int NBUF, int WM, int WN>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     const u16* __restrict__ A, const u16* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t ldc, int group_m) {
-  using P = LdsGemm<BM, BN, WM, WN>;
-  // Two stage buffers as distinct LDS objects: every access below names its
-  // buffer statically, so the compiler can tell that reads of one buffer do
-  // not depend on the DMA writes in flight to the other.
+  using P = LdsGemm<BM, BN, BK, NBUF, WM, WN>;
+  // The ring: distinct LDS objects (those past NBUF are never referenced).
   __shared__ __align__(16) char lds0[P::STAGE_BYTES];
   __shared__ __align__(16) char lds1[P::STAGE_BYTES];
+  __shared__ __align__(16) char lds2[NBUF > 2 ? P::STAGE_BYTES : 16];
+  __shared__ __align__(16) char lds3[NBUF > 3 ? P::STAGE_BYTES : 16];
+  auto buf = [&](auto I) -> char* {
+    constexpr int i = decltype(I)::value;
+    if constexpr (i == 0) return lds0;
+    else if constexpr (i == 1) return lds1;
+    else if constexpr (i == 2) return lds2;
+    else return lds3;
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -73,22 +102,23 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int nk = (K + kBK - 1) / kBK;
+  const int nk = (K + BK - 1) / BK;
 
-  // ---- global -> LDS for K step kt into buffer buf ---------------------------
-  // Physical chunk p of the A stage holds row p / 8, logical chunk
-  // (p % 8) ^ swz_a(row); of the B stage, k-row p / (BN/8), logical chunk
-  // (p % (BN/8)) ^ swz_b(row).  Instruction i of this wave fills physical
-  // chunks [64 * (wave * INSTR + i), +64), lane l the l-th of them.
-  auto dma = [&](int kt, char* st) {
-    const int k0 = kt * kBK;
+  // ---- global -> LDS for K step kt ---------------------------------------
+  // Physical chunk p of the A stage holds row p / A_ROW_CHUNKS, logical chunk
+  // (p % A_ROW_CHUNKS) ^ swz_a(row); of the B stage, k-row p / B_ROW_CHUNKS,
+  // logical chunk (p % B_ROW_CHUNKS) ^ swz_b(row).  Instruction i of this
+  // wave fills physical chunks [64 * (wave * INSTR + i), +64), lane l the
+  // l-th of them.  Steps past K load nothing (every offset out of range).
+  auto dma = [&](int kt, char* st) __attribute__((always_inline)) {
+    const int k0 = kt * BK;
     const BufRsrc ra = make_rsrc(A + (int64_t)m0 * lda + k0);
     const BufRsrc rb = make_rsrc(B + (int64_t)k0 * ldb + n0);
 #pragma unroll
     for (int i = 0; i < P::A_INSTR; ++i) {
       const int pbase = 64 * (wave * P::A_INSTR + i);
       const int p = pbase + lane;
-      const int row = p >> 3, c = (p & 7) ^ swz_a(row);
+      const int row = p / P::A_ROW_CHUNKS, c = (p % P::A_ROW_CHUNKS) ^ swz_a<BK>(row);
       const bool ok = (m0 + row < M) & (k0 + 8 * c < K);
       const uint32_t off = 2u * ((uint32_t)row * (uint32_t)lda + 8u * c);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + 16 * pbase), 16, ok ? off : kOob, 0, 0, 0);
@@ -114,7 +144,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   // Per-lane fragment addressing (bytes within a stage).
-  const int h = lane >> 5;               // which 8 of a k16 step (A) / B lane half
+  const int h = lane >> 5;
   const int g = lane >> 4, jj = lane & 15;
   int a_row[P::TM];
 #pragma unroll
@@ -126,16 +156,16 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
 
   auto a_addr = [&](int i, int ks) {
     const int row = a_row[i], c = 2 * ks + h;
-    return 16 * (row * 8 + (c ^ swz_a(row)));
+    return 16 * (row * P::A_ROW_CHUNKS + (c ^ swz_a<BK>(row)));
   };
   auto b_addr = [&](int j, int krow) {
     const int n = b_n[j];
     return P::A_BYTES + 16 * (krow * P::B_ROW_CHUNKS + ((n >> 3) ^ swz_b(krow))) + 8 * ((n >> 2) & 1);
   };
 
-  auto compute = [&](const char* st) {
+  auto compute = [&](const char* st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
+    for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8 a[P::TM], b[P::TN];
 #pragma unroll
       for (int i = 0; i < P::TM; ++i) a[i] = *reinterpret_cast<const bf16x8*>(st + a_addr(i, ks));
@@ -144,9 +174,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
         const int kr = 16 * ks + b_krow;
         const i16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(st + b_addr(j, kr)));
         const i16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(st + b_addr(j, kr + 4)));
-        typedef short i16x8v __attribute__((ext_vector_type(8)));
-        const i16x8v both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        b[j] = __builtin_bit_cast(bf16x8, both);
+        b[j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
 #pragma unroll
       for (int i = 0; i < P::TM; ++i)
@@ -155,29 +183,45 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     }
   };
 
-  // K loop unrolled by two so each half uses a fixed buffer.  The DMA of the
-  // step after next is issued unconditionally: past K its chunks are out of
-  // range and write zeros nobody reads, which keeps the body straight-line.
+  // One K step that uses ring slot I: start the loads of step kt+NBUF-1 into
+  // the slot step kt-1 used (every wave finished reading it before the last
+  // barrier), multiply step kt, then wait until this wave's loads for step
+  // kt+1 have landed (at most NBUF-2 later steps still in flight) and meet
+  // at the barrier, after which step kt+1 is in LDS for every wave.
+  // sched_barrier keeps the load issue ahead of the MFMAs it overlaps.
+  auto step = [&](auto I, int kt) __attribute__((always_inline)) {
+    constexpr int i = decltype(I)::value;
+    dma(kt + NBUF - 1, buf(std::integral_constant<int, (i + NBUF - 1) % NBUF>{}));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(buf(I));
+    wait_vmcnt<(NBUF - 2) * P::IPS>();
+    __syncthreads();
+  };
+
+  // Prologue: steps 0 .. NBUF-2 in flight, step 0 landed everywhere.
   if (nk > 0) {
     dma(0, lds0);
-    __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (NBUF > 2) dma(1, lds1);
+    if constexpr (NBUF > 3) dma(2, lds2);
+    wait_vmcnt<(NBUF - 2) * P::IPS>();
     __syncthreads();
   }
   int kt = 0;
-  // sched_barrier keeps each DMA issue ahead of the MFMAs it overlaps.
-  for (; kt + 2 <= nk; kt += 2) {
-    dma(kt + 1, lds1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(lds0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    dma(kt + 2, lds0);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(lds1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  for (; kt + NBUF <= nk; kt += NBUF) {
+    step(std::integral_constant<int, 0>{}, kt);
+    step(std::integral_constant<int, 1>{}, kt + 1);
+    if constexpr (NBUF > 2) step(std::integral_constant<int, 2>{}, kt + 2);
+    if constexpr (NBUF > 3) step(std::integral_constant<int, 3>{}, kt + 3);
   }
-  if (kt < nk) compute(lds0);
+  // Remaining steps (fewer than NBUF): same slots in order.
+  if (kt < nk) step(std::integral_constant<int, 0>{}, kt);
+  if (kt + 1 < nk) step(std::integral_constant<int, 1>{}, kt + 1);
+  if constexpr (NBUF > 2) {
+    if (kt + 2 < nk) step(std::integral_constant<int, 2>{}, kt + 2);
+  }
+  // Loads issued for steps past K still write (zeros) into LDS: let them
+  // land before this workgroup can finish and release its LDS.
+  __builtin_amdgcn_s_waitcnt(0);
 
   // Epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each block.
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
@@ -200,19 +244,21 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
 
 // Launch the LDS-DMA kernel; the caller has checked alignment (16-byte
 // operands, K, N, lda, ldb multiples of 8) and the 32-bit offset limits.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int BK, int NBUF, int WM, int WN>
 hipError_t launch_gemm_bf16_lds(const MatmulArgs& a) {
-  using P = LdsGemm<BM, BN, WM, WN>;
+  using P = LdsGemm<BM, BN, BK, NBUF, WM, WN>;
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
   if (tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_bf16_lds_kernel<BM, BN, WM, WN>), dim3((unsigned)tiles), dim3(P::NT), 0, a.stream,
-                     static_cast<const u16*>(a.x1), static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N,
-                     (int)a.K, a.ldx1, a.ldx2, a.ldo, 4);
+  hipLaunchKernelGGL((gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN>), dim3((unsigned)tiles), dim3(P::NT), 0,
+                     a.stream, static_cast<const u16*>(a.x1), static_cast<const u16*>(a.x2), a.out, (int)a.M,
+                     (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo, 4);
   return hipGetLastError();
 }
 
-template hipError_t launch_gemm_bf16_lds<256, 256, 2, 2>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<256, 128, 2, 2>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<128, 128, 2, 2>(const MatmulArgs&);
+template hipError_t launch_gemm_bf16_lds<256, 256, 32, 4, 2, 2>(const MatmulArgs&);
+template hipError_t launch_gemm_bf16_lds<256, 256, 64, 2, 2, 2>(const MatmulArgs&);
+template hipError_t launch_gemm_bf16_lds<256, 128, 64, 3, 2, 2>(const MatmulArgs&);
+template hipError_t launch_gemm_bf16_lds<256, 128, 32, 4, 2, 2>(const MatmulArgs&);
+template hipError_t launch_gemm_bf16_lds<128, 128, 64, 4, 2, 2>(const MatmulArgs&);
 
 }  // namespace tilec

@@ -83,7 +83,7 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
     }
     return find("gemm_f32_64x64x16_w2x2");
   }
-  static const char* order[] = {"gemm_bf16_256x256x64_w2x2", "gemm_bf16_128x128x64_w2x2"};
+  static const char* order[] = {"gemm_bf16_256x256x64_r2", "gemm_bf16_256x128x64_r3", "gemm_bf16_128x128x64_r4"};
   for (const char* nm : order) {
     const int v = find(nm);
     const VariantDesc* d = table()[v];
