@@ -100,7 +100,8 @@ def test_tune_features_and_shapes():
     f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8)
     assert len(f) == 16 and all(math.isfinite(x) for x in f)
     s = tune.shapes(120, seed=0)
-    assert len(s) == 120 and s == tune.shapes(120, seed=0)
+    assert len(s) == 120 + len(tune.CONFIG_SHAPES) and s == tune.shapes(120, seed=0)
+    assert set(tune.CONFIG_SHAPES) <= set(s)
     assert any(m <= 16 for m, _, _, _ in s) and any(d == "bf16" for *_, d in s)
 
 

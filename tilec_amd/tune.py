@@ -90,8 +90,18 @@ def time_ms(x1, x2, config, best=None, reps=5):
     return sorted(times)[reps // 2]
 
 
+# The BASELINE.json configurations, always part of the tuning set.
+CONFIG_SHAPES = [
+    (512, 4096, 64, "f32"),
+    (1, 4096, 4096, "f32"), (4, 4096, 4096, "f32"), (16, 4096, 4096, "f32"),
+    (1024, 1024, 1024, "f32"), (2048, 2048, 2048, "f32"), (4096, 4096, 4096, "f32"),
+    (127, 1000, 513, "f32"), (513, 3001, 127, "f32"), (1000, 4097, 3001, "f32"), (3001, 513, 1000, "f32"),
+    (8192, 8192, 8192, "bf16"), (4096, 4096, 4096, "bf16"),
+]
+
+
 def shapes(n=500, seed=0):
-    """Seeded random shapes (M, K, N, dtype).
+    """Seeded random shapes (M, K, N, dtype), plus CONFIG_SHAPES.
 
     Keeps the reference's log-uniform generator with its size limits
     (tilec/tune.py:54-65; there x1 is [M1,N] and x2 is [N,M2], so its N is
@@ -99,8 +109,8 @@ def shapes(n=500, seed=0):
     [1, 16], bf16, and ragged sizes.
     """
     rng = random.Random(seed)
-    out = set()
-    while len(out) < n:
+    out = set(CONFIG_SHAPES)
+    while len(out) < n + len(CONFIG_SHAPES):
         kind = rng.random()
         M = round(2 ** rng.uniform(7, 13))
         K = round(2 ** rng.uniform(8, 14))
@@ -118,30 +128,33 @@ def shapes(n=500, seed=0):
     return sorted(out, key=lambda s: s[0] * s[1] * s[2])
 
 
-def load():
-    with open(DATA) as f:
+def load(path=None):
+    with open(path or DATA) as f:
         return [{k: (v if k in ("chip", "dtype", "kernel") else float(v)) for k, v in r.items()}
                 for r in csv.DictReader(f)]
 
 
-def bench(n=300, seed=0):
-    """Benchmark every config of `n` shapes into DATA (resumable, flushed per shape)."""
+def bench(n=300, seed=0, path=None):
+    """Benchmark every config of `n` shapes into `path` (default DATA);
+    resumable, flushed per shape.  Inputs are N(0,1) drawn on the GPU from a
+    seeded generator (the values do not change the timings' meaning)."""
     import torch
     from . import ext
+    path = path or DATA
     chip, cus = machine()
-    done = {(int(r["M"]), int(r["K"]), int(r["N"]), r["dtype"]) for r in load()} if os.path.exists(DATA) else set()
-    with open(DATA, "a", newline="") as f:
+    done = {(int(r["M"]), int(r["K"]), int(r["N"]), r["dtype"]) for r in load(path)} if os.path.exists(path) else set()
+    with open(path, "a", newline="") as f:
         w = csv.writer(f)
         if not done:
             w.writerow(FIELDS)
-        g = torch.Generator().manual_seed(seed)
+        g = torch.Generator(device="cuda").manual_seed(seed)
         todo = shapes(n, seed)
         for i, (M, K, N, dtype) in enumerate(todo):
             if (M, K, N, dtype) in done:
                 continue
             tdt = torch.float32 if dtype == "f32" else torch.bfloat16
-            x1 = torch.randn(M, K, generator=g).to(tdt).cuda()
-            x2 = torch.randn(K, N, generator=g).to(tdt).cuda()
+            x1 = torch.randn(M, K, generator=g, device="cuda").to(tdt)
+            x2 = torch.randn(K, N, generator=g, device="cuda").to(tdt)
             best = None
             for kernel, split in ext.hip_configs(M, K, N, dtype):
                 v = _variant_by_name()[kernel]
@@ -160,12 +173,12 @@ def _key(r):
     return (int(r["M"]), int(r["K"]), int(r["N"]), r["dtype"])
 
 
-def train(test_frac=0.2, seed=0, out=MODEL):
+def train(test_frac=0.2, seed=0, out=MODEL, path=None):
     """Fit on log(ms), report held-out quality against the best config and the
     library's built-in rule, refit on everything and export JSON
     (tilec/tune.py:99-132)."""
     from sklearn.ensemble import GradientBoostingRegressor
-    rows = load()
+    rows = load(path)
     names = _variant_by_name()
     rows = [r for r in rows if r["kernel"] in names]
     keys = sorted({_key(r) for r in rows})
@@ -296,8 +309,8 @@ def _cus():
 if __name__ == "__main__":
     cmd = sys.argv[1]
     if cmd == "bench":
-        bench(int(sys.argv[2]) if len(sys.argv) > 2 else 300)
+        bench(int(sys.argv[2]) if len(sys.argv) > 2 else 300, path=sys.argv[3] if len(sys.argv) > 3 else None)
     elif cmd == "train":
         train()
     else:
-        raise SystemExit(f"usage: python -m tilec_amd.tune bench [n] | train")
+        raise SystemExit("usage: python -m tilec_amd.tune bench [n] [csv] | train")
