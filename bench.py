@@ -41,6 +41,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the skinny and bf16 sections")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
+    p.add_argument("--only", choices=["square", "skinny", "bf16", "copy"],
+                   help="run one section and print its own JSON (for profiling); 'copy' is a plain "
+                        "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
 
 
@@ -141,6 +144,29 @@ def bench_bf16(steps=10, warmup=2):
     return dict(ms=ms, TFLOPs=tflops, frac=tflops / PEAK_BF16_MFMA, config=list(cfg))
 
 
+def bench_copy(nbytes=256 << 20, reps=10):
+    """A plain device-to-device copy of known size: what FETCH_SIZE and
+    WRITE_SIZE read for it calibrates those counters."""
+    import torch
+    x = torch.ones(nbytes // 4, device="cuda")
+    y = torch.empty_like(x)
+    ms = timed(lambda: y.copy_(x), reps, 2)
+    return dict(bytes_each_way=nbytes, reps=reps, us=ms * 1e3, GBps=2 * nbytes / (ms * 1e-3) / 1e9)
+
+
+def traffic_of(kernel, M, N, K):
+    """HBM bytes per launch measured with rocprofv3 (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy calibration), as recorded in profiles/traffic.json for
+    this kernel and shape; None when it has not been measured."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(f"{kernel}@{M}x{N}x{K}")
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("bytes")
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -204,6 +230,12 @@ def main():
     _lib.lib()  # fail loudly if the HIP library is missing
     props = torch.cuda.get_device_properties(0)
 
+    if args.only:
+        out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
+               "copy": bench_copy}[args.only]()
+        print(json.dumps({"section": args.only, **out}), flush=True)
+        return
+
     sq = bench_square(args)
     extra = {}
     if not args.no_extra:
@@ -227,7 +259,8 @@ def main():
         "config": {"workload": "BASELINE config 2 at 4096^3: fp32 square GEMM, M=N=K=4096, row-major",
                    "M": 4096, "N": 4096, "K": 4096, "kernel": list(sq["config"])},
         "roofline": {"bound": "mfma", "achieved": round(sq["tflops"], 3), "peak": PEAK_FP32_MFMA,
-                     "unit": "TFLOP/s", "frac": round(sq["tflops"] / PEAK_FP32_MFMA, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(sq["tflops"] / PEAK_FP32_MFMA, 4),
+                     "traffic": traffic_of(sq["config"][0], 4096, 4096, 4096)},
         "cpu_baseline": cpu,
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "arch": getattr(props, "gcnArchName", "")},
