@@ -84,8 +84,8 @@ def hip_configs(M, K, N, dtype="f32"):
         if v["dtype"] != code or (v["max_m"] and M > v["max_m"]):
             continue
         if v["family"] == _lib.FAMILY_SKINNY:
-            # A workgroup takes at most BK rows of K (its x1 chunk lives in
-            # LDS), so small splits are raised; keep one entry per distinct
+            # A workgroup takes at most BK (the variant's K-slice cap) rows
+            # of K, so small splits are raised; keep one entry per distinct
             # effective split, each giving every wave at least one 16-row block.
             seen = set()
             for s in _SKINNY_SPLITS:
