@@ -76,11 +76,23 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM, int BN, int BK, int NBUF, int WM, int WN>
+// Scheduling groups "1 MFMA, then its share of the IPS loads", NM times.
+template <int NM, int IPS, int X = 0>
+__device__ __forceinline__ void sched_mfma_vmem() {
+  if constexpr (X < NM) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int n = (X + 1) * IPS / NM - X * IPS / NM;
+    if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x020, n, 0);
+    sched_mfma_vmem<NM, IPS, X + 1>();
+  }
+}
+
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool KFULL>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     const u16* __restrict__ A, const u16* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t ldc, int group_m) {
   using P = LdsGemm<BM, BN, BK, NBUF, WM, WN>;
+  constexpr int KS = BK / 16;  // MFMA k-slices per step
   // The ring: distinct LDS objects (those past NBUF are never referenced).
   __shared__ __align__(16) char lds0[P::STAGE_BYTES];
   __shared__ __align__(16) char lds1[P::STAGE_BYTES];
@@ -109,30 +121,49 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   // (p % A_ROW_CHUNKS) ^ swz_a(row); of the B stage, k-row p / B_ROW_CHUNKS,
   // logical chunk (p % B_ROW_CHUNKS) ^ swz_b(row).  Instruction i of this
   // wave fills physical chunks [64 * (wave * INSTR + i), +64), lane l the
-  // l-th of them.  Steps past K load nothing (every offset out of range).
-  auto dma = [&](int kt, char* st) __attribute__((always_inline)) {
+  // l-th of them.  A lane's byte offset from the step's base is the same in
+  // every step; rows past M and columns past N get kOob once, here.  When
+  // K % BK == 0 (KFULL) no other mask is needed and a step past K gets a
+  // resource of zero records, so its loads touch nothing; otherwise the
+  // k-bounds are checked per step.
+  uint32_t off_a[P::A_INSTR], off_b[P::B_INSTR];
+  int krow_b[P::B_INSTR], kcol_a[P::A_INSTR];
+#pragma unroll
+  for (int i = 0; i < P::A_INSTR; ++i) {
+    const int p = 64 * (wave * P::A_INSTR + i) + lane;
+    const int row = p / P::A_ROW_CHUNKS, c = (p % P::A_ROW_CHUNKS) ^ swz_a<BK>(row);
+    kcol_a[i] = 8 * c;
+    off_a[i] = m0 + row < M ? 2u * ((uint32_t)row * (uint32_t)lda + 8u * c) : kOob;
+  }
+#pragma unroll
+  for (int i = 0; i < P::B_INSTR; ++i) {
+    const int p = 64 * (wave * P::B_INSTR + i) + lane;
+    const int row = p / P::B_ROW_CHUNKS, c = (p % P::B_ROW_CHUNKS) ^ swz_b(row);
+    krow_b[i] = row;
+    off_b[i] = n0 + 8 * c < N ? 2u * ((uint32_t)row * (uint32_t)ldb + 8u * c) : kOob;
+  }
+  // Instruction q (0 <= q < IPS) of step kt: A instructions first, then B.
+  auto dma_one = [&](int q, int kt, char* st) __attribute__((always_inline)) {
     const int k0 = kt * BK;
-    const BufRsrc ra = make_rsrc(A + (int64_t)m0 * lda + k0);
-    const BufRsrc rb = make_rsrc(B + (int64_t)k0 * ldb + n0);
-#pragma unroll
-    for (int i = 0; i < P::A_INSTR; ++i) {
-      const int pbase = 64 * (wave * P::A_INSTR + i);
-      const int p = pbase + lane;
-      const int row = p / P::A_ROW_CHUNKS, c = (p % P::A_ROW_CHUNKS) ^ swz_a<BK>(row);
-      const bool ok = (m0 + row < M) & (k0 + 8 * c < K);
-      const uint32_t off = 2u * ((uint32_t)row * (uint32_t)lda + 8u * c);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + 16 * pbase), 16, ok ? off : kOob, 0, 0, 0);
+    const uint32_t recs = kt < nk ? 0x7FFFFFFFu : 0u;
+    if (q < P::A_INSTR) {
+      const BufRsrc ra = make_rsrc(A + (int64_t)m0 * lda + k0, recs);
+      uint32_t off = off_a[q];
+      if constexpr (!KFULL) off = k0 + kcol_a[q] < K ? off : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + 16 * 64 * (wave * P::A_INSTR + q)), 16, off, 0,
+                                               0, 0);
+    } else {
+      const int i = q - P::A_INSTR;
+      const BufRsrc rb = make_rsrc(B + (int64_t)k0 * ldb + n0, recs);
+      uint32_t off = off_b[i];
+      if constexpr (!KFULL) off = k0 + krow_b[i] < K ? off : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(st + P::A_BYTES + 16 * 64 * (wave * P::B_INSTR + i)),
+                                               16, off, 0, 0, 0);
     }
+  };
+  auto dma = [&](int kt, char* st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < P::B_INSTR; ++i) {
-      const int pbase = 64 * (wave * P::B_INSTR + i);
-      const int p = pbase + lane;
-      const int row = p / P::B_ROW_CHUNKS, c = (p % P::B_ROW_CHUNKS) ^ swz_b(row);
-      const bool ok = (k0 + row < K) & (n0 + 8 * c < N);
-      const uint32_t off = 2u * ((uint32_t)row * (uint32_t)ldb + 8u * c);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(st + P::A_BYTES + 16 * pbase), 16, ok ? off : kOob,
-                                               0, 0, 0);
-    }
+    for (int q = 0; q < P::IPS; ++q) dma_one(q, kt, st);
   };
 
   f32x16 acc[P::TM][P::TN];
@@ -163,48 +194,91 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     return P::A_BYTES + 16 * (krow * P::B_ROW_CHUNKS + ((n >> 3) ^ swz_b(krow))) + 8 * ((n >> 2) & 1);
   };
 
-  auto compute = [&](const char* st) __attribute__((always_inline)) {
+  // The operands of one k-slice: A rows of the wave's 32-row blocks, B
+  // columns of its 32-column blocks (8 consecutive k each).
+  struct Frag {
+    bf16x8 a[P::TM], b[P::TN];
+  };
+  auto read = [&](const char* st, int ks, Frag& f) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 a[P::TM], b[P::TN];
+    for (int i = 0; i < P::TM; ++i) f.a[i] = *reinterpret_cast<const bf16x8*>(st + a_addr(i, ks));
 #pragma unroll
-      for (int i = 0; i < P::TM; ++i) a[i] = *reinterpret_cast<const bf16x8*>(st + a_addr(i, ks));
-#pragma unroll
-      for (int j = 0; j < P::TN; ++j) {
-        const int kr = 16 * ks + b_krow;
-        const i16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(st + b_addr(j, kr)));
-        const i16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(st + b_addr(j, kr + 4)));
-        b[j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      }
-#pragma unroll
-      for (int i = 0; i < P::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < P::TN; ++j) acc[i][j] = mfma32x32x16bf16(a[i], b[j], acc[i][j]);
+    for (int j = 0; j < P::TN; ++j) {
+      const int kr = 16 * ks + b_krow;
+      const i16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(st + b_addr(j, kr)));
+      const i16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(st + b_addr(j, kr + 4)));
+      f.b[j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   };
-
-  // One K step that uses ring slot I: start the loads of step kt+NBUF-1 into
-  // the slot step kt-1 used (every wave finished reading it before the last
-  // barrier), multiply step kt, then wait until this wave's loads for step
-  // kt+1 have landed (at most NBUF-2 later steps still in flight) and meet
-  // at the barrier, after which step kt+1 is in LDS for every wave.
-  // sched_barrier keeps the load issue ahead of the MFMAs it overlaps.
-  auto step = [&](auto I, int kt) __attribute__((always_inline)) {
-    constexpr int i = decltype(I)::value;
-    dma(kt + NBUF - 1, buf(std::integral_constant<int, (i + NBUF - 1) % NBUF>{}));
-    __builtin_amdgcn_sched_barrier(0);
-    compute(buf(I));
-    wait_vmcnt<(NBUF - 2) * P::IPS>();
-    __syncthreads();
+  auto mma = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < P::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < P::TN; ++j) acc[i][j] = mfma32x32x16bf16(f.a[i], f.b[j], acc[i][j]);
+  };
+  // The MFMAs of f with the loads of step kt threaded between them, so the
+  // loads issue while the matrix cores are busy.
+  auto mma_dma = [&](const Frag& f, int kt, char* st) __attribute__((always_inline)) {
+    constexpr int NM = P::TM * P::TN;
+#pragma unroll
+    for (int x = 0; x < NM; ++x) {
+      const int i = x / P::TN, j = x % P::TN;
+      acc[i][j] = mfma32x32x16bf16(f.a[i], f.b[j], acc[i][j]);
+#pragma unroll
+      for (int q = x * P::IPS / NM; q < (x + 1) * P::IPS / NM; ++q) dma_one(q, kt, st);
+    }
+    sched_mfma_vmem<NM, P::IPS>();
   };
 
-  // Prologue: steps 0 .. NBUF-2 in flight, step 0 landed everywhere.
+  // Software pipeline over K steps.  Entering step kt (ring slot I): f[0]
+  // holds (or is loading) k-slice 0 of step kt; f[1] holds the last k-slice
+  // of step kt-1, whose MFMAs have not been issued (zeros before step 0).
+  // Step kt:
+  //   1. MFMAs of f[1], threaded with the loads of step kt+NBUF-1 into the
+  //      slot step kt-1 used — every wave finished reading that slot before
+  //      the last barrier — so the matrix cores stay busy across it;
+  //   2. k-slices 0 .. KS-2 of step kt, each one's MFMAs overlapping the LDS
+  //      reads of the next; the last k-slice is read into f[1];
+  //   3. wait for those reads and for this wave's loads of step kt+1 (at most
+  //      NBUF-2 later steps in flight; loads complete in issue order), then
+  //      the barrier: step kt+1 is in LDS for every wave and no wave reads
+  //      step kt's slot again;
+  //   4. read k-slice 0 of step kt+1 into f[0].
+  Frag f[2];
+#pragma unroll
+  for (int i = 0; i < P::TM; ++i) f[1].a[i] = bf16x8{};
+#pragma unroll
+  for (int j = 0; j < P::TN; ++j) f[1].b[j] = bf16x8{};
+
+  constexpr int WAIT = (NBUF - 2) * P::IPS;
+  auto step = [&](auto I, int kt) __attribute__((always_inline)) {
+    constexpr int i = decltype(I)::value;
+    char* const cur = buf(I);
+    mma_dma(f[1], kt + NBUF - 1, buf(std::integral_constant<int, (i + NBUF - 1) % NBUF>{}));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      read(cur, ks + 1, f[(ks + 1) & 1]);
+      mma(f[ks & 1]);
+    }
+    // The step's MFMAs stay ahead of the wait: nothing crosses this point.
+    __builtin_amdgcn_sched_barrier(0);
+    // vmcnt(WAIT) lgkmcnt(0) (gfx9 encoding, expcnt unconstrained)
+    __builtin_amdgcn_s_waitcnt((WAIT & 15) | ((WAIT >> 4) << 14) | (7 << 4));
+    __syncthreads();
+    read(buf(std::integral_constant<int, (i + 1) % NBUF>{}), 0, f[0]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: steps 0 .. NBUF-2 in flight, step 0 landed everywhere, its
+  // first k-slice being read.
   if (nk > 0) {
     dma(0, lds0);
     if constexpr (NBUF > 2) dma(1, lds1);
     if constexpr (NBUF > 3) dma(2, lds2);
-    wait_vmcnt<(NBUF - 2) * P::IPS>();
+    wait_vmcnt<WAIT>();
     __syncthreads();
+    read(lds0, 0, f[0]);
   }
   int kt = 0;
   for (; kt + NBUF <= nk; kt += NBUF) {
@@ -219,6 +293,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   if constexpr (NBUF > 2) {
     if (kt + 2 < nk) step(std::integral_constant<int, 2>{}, kt + 2);
   }
+  mma(f[1]);  // last k-slice of the last step (zeros if K == 0)
   // Loads issued for steps past K still write (zeros) into LDS: let them
   // land before this workgroup can finish and release its LDS.
   __builtin_amdgcn_s_waitcnt(0);
@@ -249,9 +324,10 @@ hipError_t launch_gemm_bf16_lds(const MatmulArgs& a) {
   using P = LdsGemm<BM, BN, BK, NBUF, WM, WN>;
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
   if (tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN>), dim3((unsigned)tiles), dim3(P::NT), 0,
-                     a.stream, static_cast<const u16*>(a.x1), static_cast<const u16*>(a.x2), a.out, (int)a.M,
-                     (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo, 4);
+  auto kern = a.K % BK == 0 ? gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, true>
+                            : gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(P::NT), 0, a.stream, static_cast<const u16*>(a.x1),
+                     static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo, 4);
   return hipGetLastError();
 }
 
