@@ -205,9 +205,10 @@ namespace {
 
 // Aligned operands (16-byte base, K, N, lda, ldb multiples of 8) whose tile
 // offsets fit 32 bits run the LDS-DMA kernel of gemm_bf16_lds.hip with a
-// ring of NBUF stage buffers of BK; everything else runs the generic kernel
-// above with the same output tile (NBUF == 0: generic kernel only).
-template <int BM, int BN, int BK, int NBUF>
+// ring of NBUF stage buffers of BK and WM x WN waves; everything else runs
+// the generic kernel above (2 x 2 waves) with the same output tile
+// (NBUF == 0: generic kernel only).
+template <int BM, int BN, int BK, int NBUF, int WM = 2, int WN = 2>
 hipError_t launch_gemm_bf16(const MatmulArgs& a) {
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
   if (tiles == 0) return hipSuccess;
@@ -215,7 +216,7 @@ hipError_t launch_gemm_bf16(const MatmulArgs& a) {
                    (reinterpret_cast<uintptr_t>(a.x1) % 16 == 0) && (reinterpret_cast<uintptr_t>(a.x2) % 16 == 0);
   if constexpr (NBUF > 0) {
     if (vec && a.ldx1 < (int64_t(1) << 22) && a.ldx2 < (int64_t(1) << 24))
-      return launch_gemm_bf16_lds<BM, BN, BK, NBUF, 2, 2>(a);
+      return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN>(a);
   }
   dim3 grid((unsigned)tiles);
   return vec ? launch_one<BM, BN, 64, 2, 2, true>(a, grid) : launch_one<BM, BN, 64, 2, 2, false>(a, grid);
@@ -229,14 +230,14 @@ const VariantDesc* gemm_bf16_variants(int* count) {
   static const VariantDesc t[] = {
       {"gemm_bf16_256x256x32_r4", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 32, 4, 0, 4,
        launch_gemm_bf16<256, 256, 32, 4>},
-      {"gemm_bf16_256x256x64_r2", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 64, 4, 0, 2,
-       launch_gemm_bf16<256, 256, 64, 2>},
-      {"gemm_bf16_256x128x64_r3", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 128, 64, 4, 0, 3,
-       launch_gemm_bf16<256, 128, 64, 3>},
+      {"gemm_bf16_256x256x64_r2", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 64, 8, 0, 2,
+       launch_gemm_bf16<256, 256, 64, 2, 2, 4>},
+      {"gemm_bf16_256x128x64_r3", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 128, 64, 8, 0, 3,
+       launch_gemm_bf16<256, 128, 64, 3, 4, 2>},
       {"gemm_bf16_256x128x32_r4", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 128, 32, 4, 0, 4,
        launch_gemm_bf16<256, 128, 32, 4>},
-      {"gemm_bf16_128x128x64_r4", TILEC_FAMILY_GEMM, TILEC_BF16, 128, 128, 64, 4, 0, 4,
-       launch_gemm_bf16<128, 128, 64, 4>},
+      {"gemm_bf16_128x128x64_r4", TILEC_FAMILY_GEMM, TILEC_BF16, 128, 128, 64, 8, 0, 4,
+       launch_gemm_bf16<128, 128, 64, 4, 2, 4>},
       {"gemm_bf16_64x64x64_w2x2", TILEC_FAMILY_GEMM, TILEC_BF16, 64, 64, 64, 4, 0, 1,
        launch_gemm_bf16<64, 64, 64, 0>},
   };

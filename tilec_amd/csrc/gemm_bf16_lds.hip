@@ -24,6 +24,11 @@
 //     buffer offset and land in LDS as zeros.  Operands must be 16-byte
 //     aligned with K, N, lda, ldb multiples of 8 (the launcher checks; other
 //     shapes go to the generic kernel in gemm_bf16.hip).
+//   * Per K step, the MFMAs of the previous step's last k-slice (read into
+//     registers before the barrier) run right after it, threaded one-for-one
+//     with the next step's loads, so neither the barrier nor the load issue
+//     leaves the matrix cores idle.  With 8 waves (2 per SIMD) one wave's
+//     MFMAs also cover the other's LDS waits.
 //   * XCD-aware grouped tile order (tile_of in common.h).
 #include "common.h"
 #include "../../include/tilec.h"
@@ -332,9 +337,9 @@ hipError_t launch_gemm_bf16_lds(const MatmulArgs& a) {
 }
 
 template hipError_t launch_gemm_bf16_lds<256, 256, 32, 4, 2, 2>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<256, 256, 64, 2, 2, 2>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<256, 128, 64, 3, 2, 2>(const MatmulArgs&);
+template hipError_t launch_gemm_bf16_lds<256, 256, 64, 2, 2, 4>(const MatmulArgs&);
+template hipError_t launch_gemm_bf16_lds<256, 128, 64, 3, 4, 2>(const MatmulArgs&);
 template hipError_t launch_gemm_bf16_lds<256, 128, 32, 4, 2, 2>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<128, 128, 64, 4, 2, 2>(const MatmulArgs&);
+template hipError_t launch_gemm_bf16_lds<128, 128, 64, 4, 2, 4>(const MatmulArgs&);
 
 }  // namespace tilec
