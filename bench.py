@@ -13,6 +13,8 @@ warmup steps.  Extra objects in the same line:
                  beyond the 256 MB Infinity Cache), launches replayed from a
                  HIP graph so the host does not bound an 8 us kernel
   bf16_8192    — config 4, bf16 8192^3 with fp32 accumulate, vs 2.5 PFLOP/s
+  configs      — every fp32 config (0, 2 at 1024/2048/4096, the 4 ragged
+                 shapes of 3): device time per call from graph replay
   cpu_baseline — the oracle's tiled C restatement of the reference kernel
                  (oracle/matmul_oracle.c, OpenMP) on a bounded row sample of
                  the same 4096^3 problem, on this box's host cores; plus
@@ -41,7 +43,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the skinny and bf16 sections")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
-    p.add_argument("--only", choices=["square", "skinny", "bf16", "copy"],
+    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "copy"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -144,6 +146,52 @@ def bench_bf16(steps=10, warmup=2):
     return dict(ms=ms, TFLOPs=tflops, frac=tflops / PEAK_BF16_MFMA, config=list(cfg))
 
 
+CONFIG_CASES = (
+    # (name, M, K, N, generator): BASELINE configs 0, 2 and 3 (fp32)
+    ("readme_512x4096x64", 512, 4096, 64, "normal"),
+    ("square_1024", 1024, 1024, 1024, "uniform"),
+    ("square_2048", 2048, 2048, 2048, "uniform"),
+    ("square_4096", 4096, 4096, 4096, "uniform"),
+    ("ragged_127x1000x513", 127, 1000, 513, "normal"),
+    ("ragged_513x3001x127", 513, 3001, 127, "normal"),
+    ("ragged_1000x4097x3001", 1000, 4097, 3001, "normal"),
+    ("ragged_3001x513x1000", 3001, 513, 1000, "normal"),
+)
+
+
+def bench_configs(reps=20):
+    """Every fp32 BASELINE config: device time per call from a HIP graph of
+    `reps` calls (so small, latency-bound shapes are not timed as host
+    overhead), TFLOP/s and the fraction of the fp32 matrix peak."""
+    import torch
+    from oracle import oracle as O
+    from tilec_amd import ext
+    out = {}
+    for i, (name, M, K, N, gen) in enumerate(CONFIG_CASES):
+        draw = O.uniform if gen == "uniform" else O.normal
+        x1 = torch.from_numpy(draw((M, K), 100 + 2 * i)).cuda()
+        x2 = torch.from_numpy(draw((K, N), 101 + 2 * i)).cuda()
+        cfg = kernel_name_for(M, K, N, "f32")
+        ext.matrix_mul(x1, x2)  # workspace exists before capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            ext.matrix_mul(x1, x2)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                outs = [ext.matrix_mul(x1, x2) for _ in range(reps)]
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            ms = timed(g.replay, 3, 1, stream=s) / reps
+        del outs
+        tflops = 2 * M * N * K / (ms * 1e-3) / 1e12
+        out[name] = dict(us=ms * 1e3, TFLOPs=tflops, frac=tflops / PEAK_FP32_MFMA, config=list(cfg))
+        log(f"{name}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s ({cfg})")
+    return out
+
+
 def bench_copy(nbytes=256 << 20, reps=10):
     """A plain device-to-device copy of known size: what FETCH_SIZE and
     WRITE_SIZE read for it calibrates those counters."""
@@ -232,7 +280,7 @@ def main():
 
     if args.only:
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
-               "copy": bench_copy}[args.only]()
+               "configs": bench_configs, "copy": bench_copy}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return
 
@@ -241,6 +289,7 @@ def main():
     if not args.no_extra:
         extra["skinny"] = bench_skinny()
         extra["bf16_8192"] = bench_bf16()
+        extra["configs"] = bench_configs()
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
 
     rec = {

@@ -49,7 +49,8 @@ extern "C" {
 #define TILEC_BF16 1
 
 /* Kernel families (tilec_variant_info, info[0]). */
-#define TILEC_FAMILY_SKINNY 0 /* output-stationary streaming kernel, M <= 16  */
+#define TILEC_FAMILY_SKINNY 0 /* output-stationary streaming kernel, split K:   */
+                              /* M <= 16, or outputs of few 64x64 tiles         */
 #define TILEC_FAMILY_GEMM 1   /* LDS-staged MFMA tile GEMM                      */
 
 /* Pass as `variant` to let the library pick with its built-in rule. */

@@ -87,13 +87,13 @@ def test_hip_configs_rules():
             v = names[name]
             assert v["dtype"] == (_lib.F32 if dt == "f32" else _lib.BF16)
             if v["family"] == _lib.FAMILY_SKINNY:
-                assert M <= v["max_m"]
+                assert v["max_m"] == 0 or M <= v["max_m"]
                 eff = ext._skinny_splits(K, s, v["bk"])
                 assert eff == 1 or K // eff >= 16 * v["waves"]
             else:
                 assert s == 1
         has_skinny = any(names[n]["family"] == _lib.FAMILY_SKINNY for n, _ in cfgs)
-        assert has_skinny == (M <= 16 and dt == "f32")
+        assert has_skinny == (ext.skinny_regime(M, N) and dt == "f32")
 
 
 def test_tune_features_and_shapes():
@@ -190,7 +190,9 @@ def test_abi_rejects_bad_arguments_before_launch():
     skinny = _lib.variant_id("skinny_f32_w8_b1")
     gemm = _lib.variant_id("gemm_f32_128x128x16_w2x2")
     bf16 = _lib.variant_id("gemm_bf16_128x128x64_r4")
-    assert _call(M=17, variant=skinny) == _lib.ERR_UNSUPPORTED
+    # The streaming kernel takes any M in 16-row blocks, up to 65535 of them.
+    assert _call(M=16 * 65535 + 1, variant=skinny) == _lib.ERR_UNSUPPORTED
+    assert "M <=" in _lib.last_error()
     assert _call(variant=bf16, dtype=0) == _lib.ERR_UNSUPPORTED
     assert _call(variant=gemm, split=2) == _lib.ERR_UNSUPPORTED
     # Split K needs a workspace.

@@ -135,6 +135,30 @@ def test_skinny_shapes_and_splits():
             say(f"skinny m={m} k={k} n={n} ok")
 
 
+def test_skinny_row_blocks():
+    """M > 16 on the streaming kernel: one grid row block per 16 rows of x1,
+    each with its own partial slots and counters (every skinny config the
+    tuner may pick for these small outputs)."""
+    for i, (m, k, n) in enumerate([(17, 64, 64), (40, 1000, 65), (127, 1000, 513), (513, 3001, 127),
+                                   (512, 4096, 64)]):
+        a, b = O.normal((m, k), 500 + 2 * i), O.normal((k, n), 501 + 2 * i)
+        ref = O.matmul_f64(a, b)
+        cfgs = [c for c in ext.hip_configs(m, k, n, "f32") if c[0].startswith("skinny")]
+        assert cfgs, (m, k, n)
+        for cfg in cfgs:
+            got = run(dev(a), dev(b), cfg)
+            assert O.rel_l2(got, ref) <= O.TOL_F32, (cfg, (m, k, n))
+        say(f"skinny row blocks m={m} k={k} n={n}: {len(cfgs)} configs ok")
+    # Bit-exact on small integers (every partial sum exact in fp32), ragged
+    # last row block and slab.
+    rng = np.random.default_rng(11)
+    a = rng.integers(-3, 4, (37, 777)).astype(np.float32)
+    b = rng.integers(-3, 4, (777, 131)).astype(np.float32)
+    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    for cfg in [("skinny_f32_w4_b1", 3), ("skinny_f32_w8_b2", 8), ("skinny_f32_w16_b1", 1)]:
+        np.testing.assert_array_equal(run(dev(a), dev(b), cfg), want)
+
+
 # ---------------------------------------------------------------------------
 # BASELINE.json configs (seeds 2i / 2i+1 for config i)
 # ---------------------------------------------------------------------------

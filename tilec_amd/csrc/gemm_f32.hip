@@ -38,6 +38,10 @@ struct GemmF32 {
   static constexpr size_t kLds = sizeof(float) * 2 * BK * (LDA_S + LDB_S);
 };
 
+// Four consecutive floats at a 4-byte aligned address: one dwordx4 load,
+// which CDNA performs for any dword-aligned address.
+typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
 template <bool VEC>
 __device__ __forceinline__ f32x4 ld4(const float* __restrict__ p, bool ok_all, int valid) {
   // valid: number of leading elements in bounds (0..4); VEC => valid in {0,4}
@@ -85,8 +89,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
       const int e = tid + p * P::NT;
       const int i = e / (BK / 4), kq = e % (BK / 4);
       const int gm = m0 + i, gk = k0 + 4 * kq;
-      if (!mask) {
-        ra[p] = ld4<VEC>(A + (int64_t)gm * lda + gk, true, 4);
+      if (!mask) {  // whole quad in bounds: one (dword-aligned) 16-byte load
+        ra[p] = *reinterpret_cast<const f32x4_a4*>(A + (int64_t)gm * lda + gk);
       } else {
         const bool rok = gm < M;
         const int valid = rok ? max(0, min(4, K - gk)) : 0;
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
       const int k = e / (BN / 4), jq = e % (BN / 4);
       const int gk = k0 + k, gn = n0 + 4 * jq;
       if (!mask) {
-        rb[p] = ld4<VEC>(B + (int64_t)gk * ldb + gn, true, 4);
+        rb[p] = *reinterpret_cast<const f32x4_a4*>(B + (int64_t)gk * ldb + gn);
       } else {
         const int valid = gk < K ? max(0, min(4, N - gn)) : 0;
         const int64_t off = valid > 0 ? (int64_t)gk * ldb + gn : 0;

@@ -1,5 +1,8 @@
-// Output-stationary streaming kernel for skinny products, M <= 16:
+// Output-stationary streaming kernel for products with a small output:
 //   out[M,N] = x1[M,K] · x2[K,N]   (fp32 in, fp32 out)
+// built for M <= 16 (one 16-row block) and used for any M whose output is
+// too small to fill the chip with tile-GEMM workgroups (each further 16 rows
+// of x1 is one more row block of the grid).
 //
 // Replaces, for small M, the reference's threadgroup-split dot product with a
 // SIMD-group reduction (the legacy `_matrix_mul` described at README.md:57,73,
@@ -23,11 +26,12 @@
 // 4 KiB of x2 a wave issues 16 MFMAs (512 cycles), 2.5x the rate the HBM
 // share of a SIMD needs, for any M <= 16.
 //
-// Grid: x = 64-column slabs, y = K splits.  Waves are summed through LDS;
-// with a split K each workgroup writes its [M x 64] partial to the
-// workspace, and the last workgroup of a slab to finish (completion counter)
-// adds the partials in split order, so results do not depend on scheduling;
-// it resets the counter to zero.
+// Grid: x = 64-column slabs, y = K splits, z = 16-row blocks of x1 and out.
+// Waves are summed through LDS; with a split K each workgroup writes its
+// [16 x 64] partial to the workspace, and the last workgroup of a (row
+// block, slab) to finish (completion counter) adds the partials in split
+// order, so results do not depend on scheduling; it resets the counter to
+// zero.
 #include "common.h"
 #include "../../include/tilec.h"
 
@@ -42,14 +46,15 @@ constexpr int kKcMax = 1024;   // rows per K chunk at most
 constexpr int kCounterStride = 64;  // uint32s between completion counters (own 256-byte line each)
 
 struct SkinnyGeom {
-  int64_t nslabs, splits, kc;
+  int64_t nslabs, splits, kc, nrb;
 };
 
 // K chunk per split: a multiple of kBlock rows, at most kKcMax; the number of
 // splits is raised to what kKcMax needs and recomputed so that none is empty.
-SkinnyGeom skinny_geom(int64_t N, int64_t K, int split_k) {
+SkinnyGeom skinny_geom(int64_t M, int64_t N, int64_t K, int split_k) {
   SkinnyGeom g;
   g.nslabs = cdiv(N, kSlab);
+  g.nrb = cdiv(M, kMaxM);
   if (K <= 0) {
     g.splits = 1;
     g.kc = 0;
@@ -83,7 +88,7 @@ struct Block {
 template <int WAVES, int UB, bool VEC>
 __global__ __launch_bounds__(WAVES * 64) void skinny_f32_kernel(
     const float* __restrict__ x1, const float* __restrict__ x2, float* __restrict__ out,
-    int M, int N, int K, int64_t ldx1, int64_t ldx2, int64_t ldo, int kc,
+    int M_all, int N, int K, int64_t ldx1, int64_t ldx2, int64_t ldo, int kc,
     unsigned* __restrict__ counters, float* __restrict__ part) {
   __shared__ f32x4 red[WAVES * kMaxM * 16];  // [wave][row][quad]
   __shared__ int last_flag;
@@ -92,8 +97,13 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f32_kernel(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int r = lane >> 4, q = lane & 15;
-  const int slab = blockIdx.x, split = blockIdx.y;
+  const int slab = blockIdx.x, split = blockIdx.y, rb = blockIdx.z;
   const int nslabs = gridDim.x, S = gridDim.y;
+  // This workgroup's row block: rows 16*rb .. of x1 and out, M of them.
+  const int M = min(kMaxM, M_all - kMaxM * rb);
+  x1 += (int64_t)kMaxM * rb * ldx1;
+  out += (int64_t)kMaxM * rb * ldo;
+  const int cell = rb * nslabs + slab;  // (row block, slab): partial slot and counter
   const int col = slab * kSlab + 4 * q;
   const bool col_ok = col < N;
   const int kbeg = split * kc;
@@ -109,26 +119,26 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f32_kernel(
   const bool a_row = q < M;
   auto load_block = [&](int b, Block& blk) {
     const int brow = 16 * b;  // wave-uniform, relative to kbeg
-    const BufRsrc rb = make_rsrc(x2 + (int64_t)(kbeg + brow) * ldx2);
-    const BufRsrc ra = make_rsrc(x1 + kbeg + brow);
+    const BufRsrc rx2 = make_rsrc(x2 + (int64_t)(kbeg + brow) * ldx2);
+    const BufRsrc rx1 = make_rsrc(x1 + kbeg + brow);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int row = 4 * r + u;
       const bool ok = brow + row < nrows;
       const uint32_t roff = 4u * (uint32_t)row * (uint32_t)ldx2;
       if (VEC) {
-        blk.b[u] = load_f32x4(rb, (ok & col_ok) ? roff + col_off : kOob);
+        blk.b[u] = load_f32x4(rx2, (ok & col_ok) ? roff + col_off : kOob);
       } else {
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-          blk.b[u][c] = load_f32(rb, (ok & (col + c < N)) ? roff + col_off + 4u * c : kOob);
+          blk.b[u][c] = load_f32(rx2, (ok & (col + c < N)) ? roff + col_off + 4u * c : kOob);
       }
     }
     if (VEC) {  // K % 4 == 0: the 4 rows of a quad are all valid or all past the chunk
-      blk.a = load_f32x4(ra, (a_row & (brow + 4 * r < nrows)) ? a_off : kOob);
+      blk.a = load_f32x4(rx1, (a_row & (brow + 4 * r < nrows)) ? a_off : kOob);
     } else {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) blk.a[u] = load_f32(ra, (a_row & (brow + 4 * r + u < nrows)) ? a_off + 4u * u : kOob);
+      for (int u = 0; u < 4; ++u) blk.a[u] = load_f32(rx1, (a_row & (brow + 4 * r + u < nrows)) ? a_off + 4u * u : kOob);
     }
   };
 
@@ -209,8 +219,8 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f32_kernel(
   // for its partial store to complete (vmcnt(0)) before the barrier; wave 0
   // then bumps the slab's counter with an agent-scope atomic; the workgroup
   // that brings it to S reads the partials after seeing that value.
-  const BufRsrc prs = make_rsrc(part + (int64_t)slab * kMaxM * kSlab);
-  const uint32_t split_stride = 4u * (uint32_t)nslabs * kMaxM * kSlab;  // bytes between splits
+  const BufRsrc prs = make_rsrc(part + (int64_t)cell * kMaxM * kSlab);
+  const uint32_t split_stride = 4u * (uint32_t)(gridDim.z * nslabs) * kMaxM * kSlab;  // bytes between splits
   const uint32_t item_off = 4u * (uint32_t)(m * kSlab + 4 * cq);
   if (mine) store_f32x4_coherent(prs, (uint32_t)split * split_stride + item_off, sum);
   __builtin_amdgcn_s_waitcnt(0);
@@ -218,33 +228,49 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f32_kernel(
   if (wave == 0) {
     unsigned prev = 0;
     if (lane == 0)
-      prev = __hip_atomic_fetch_add(&counters[slab * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      prev = __hip_atomic_fetch_add(&counters[cell * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     prev = (unsigned)__shfl((int)prev, 0);
     if (lane == 0) last_flag = prev == (unsigned)(S - 1);
   }
   __syncthreads();
   if (!last_flag) return;
 
-  // Partials of split sp for this slab start at (sp * nslabs + slab) * 1024
-  // floats; 8 splits are loaded at once, then added in split order.
-  if (mine) {
+  // Partials of split sp for this cell start at (sp * cells + cell) * 1024
+  // floats.  The M*16 live items are spread over the whole workgroup: thread
+  // t = g*items + item adds the contiguous split range [g*S/G, (g+1)*S/G) of
+  // its item, up to 8 loads in flight, so any S costs about one memory round
+  // trip; the G group sums then meet in LDS and are added in group order.
+  // The order of additions depends only on S, M and the block size.
+  if (tid == 0) __hip_atomic_store(&counters[cell * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int items = M * 16;
+  const int G = min(S, (WAVES * 64) / items);
+  const int g = tid / items, it = tid - g * items;
+  const int im = it >> 4, icq = it & 15;
+  if (g < G) {
+    const int s_beg = (g * S) / G, s_end = ((g + 1) * S) / G;
+    const uint32_t off = 4u * (uint32_t)(im * kSlab + 4 * icq);
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < S; s0 += 8) {
+    for (int s0 = s_beg; s0 < s_end; s0 += 8) {
       f32x4 v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        v[j] = load_f32x4_coherent(prs, s0 + j < S ? (uint32_t)(s0 + j) * split_stride + item_off : kOob);
+        v[j] = load_f32x4_coherent(prs, s0 + j < s_end ? (uint32_t)(s0 + j) * split_stride + off : kOob);
 #pragma unroll
       for (int j = 0; j < 8; ++j) t += v[j];
     }
-    store_quad<VEC>(out + (int64_t)m * ldo, ocol, N, t);
+    red[tid] = t;  // red[g * items + it]; every read of red above finished before the last barrier
   }
-  if (tid == 0) __hip_atomic_store(&counters[slab * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (tid < items) {
+    f32x4 t = red[tid];
+    for (int j = 1; j < G; ++j) t += red[j * items + tid];
+    store_quad<VEC>(out + (int64_t)im * ldo, slab * kSlab + 4 * icq, N, t);
+  }
 }
 
 template <int WAVES, int UB, bool VEC>
 hipError_t launch_one(const MatmulArgs& a, const SkinnyGeom& g, unsigned* counters, float* part) {
-  hipLaunchKernelGGL((skinny_f32_kernel<WAVES, UB, VEC>), dim3((unsigned)g.nslabs, (unsigned)g.splits),
+  hipLaunchKernelGGL((skinny_f32_kernel<WAVES, UB, VEC>), dim3((unsigned)g.nslabs, (unsigned)g.splits, (unsigned)g.nrb),
                      dim3(WAVES * 64), 0, a.stream, static_cast<const float*>(a.x1),
                      static_cast<const float*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo,
                      (int)g.kc, counters, part);
@@ -253,7 +279,7 @@ hipError_t launch_one(const MatmulArgs& a, const SkinnyGeom& g, unsigned* counte
 
 template <int WAVES, int UB>
 hipError_t launch_skinny(const MatmulArgs& a) {
-  const SkinnyGeom g = skinny_geom(a.N, a.K, a.split_k);
+  const SkinnyGeom g = skinny_geom(a.M, a.N, a.K, a.split_k);
   const bool vec = (a.N % 4 == 0) && (a.ldx2 % 4 == 0) && (a.ldo % 4 == 0) && (a.K % 4 == 0) &&
                    (a.ldx1 % 4 == 0) && (reinterpret_cast<uintptr_t>(a.x1) % 16 == 0) &&
                    (reinterpret_cast<uintptr_t>(a.x2) % 16 == 0) &&
@@ -267,33 +293,33 @@ hipError_t launch_skinny(const MatmulArgs& a) {
 }  // namespace
 
 // Variant table for this family (its order is part of the variant numbering).
-// BM = rows (M <= 16), BN = slab width, BK = the largest K chunk of one
-// workgroup, unroll = 16-row blocks per batch.
+// BM = rows per row block, BN = slab width, BK = the largest K chunk of one
+// workgroup, unroll = 16-row blocks per batch; max_m 0 = any M.
 const VariantDesc* skinny_variants(int* count) {
   static const VariantDesc t[] = {
-      {"skinny_f32_w4_b1", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 4, kMaxM, 1, launch_skinny<4, 1>},
-      {"skinny_f32_w4_b2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 4, kMaxM, 2, launch_skinny<4, 2>},
-      {"skinny_f32_w8_b1", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 8, kMaxM, 1, launch_skinny<8, 1>},
-      {"skinny_f32_w8_b2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 8, kMaxM, 2, launch_skinny<8, 2>},
-      {"skinny_f32_w16_b1", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 16, kMaxM, 1, launch_skinny<16, 1>},
+      {"skinny_f32_w4_b1", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 4, 0, 1, launch_skinny<4, 1>},
+      {"skinny_f32_w4_b2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 4, 0, 2, launch_skinny<4, 2>},
+      {"skinny_f32_w8_b1", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 8, 0, 1, launch_skinny<8, 1>},
+      {"skinny_f32_w8_b2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 8, 0, 2, launch_skinny<8, 2>},
+      {"skinny_f32_w16_b1", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlab, kKcMax, 16, 0, 1, launch_skinny<16, 1>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;
 }
 
-// Split K needs partials [splits][nslabs][16][64] fp32 (scratch) and one
-// completion counter per slab, each on its own 256-byte line so workgroups of
-// different slabs do not contend on one line.
-size_t skinny_counter_bytes(int64_t N, int64_t K, int split_k) {
-  const SkinnyGeom g = skinny_geom(N, K, split_k);
+// Split K needs partials [splits][row blocks][slabs][16][64] fp32 (scratch)
+// and one completion counter per (row block, slab), each on its own 256-byte
+// line so workgroups of different cells do not contend on one line.
+size_t skinny_counter_bytes(int64_t M, int64_t N, int64_t K, int split_k) {
+  const SkinnyGeom g = skinny_geom(M, N, K, split_k);
   if (g.splits <= 1) return 0;
-  return (size_t)g.nslabs * kCounterStride * sizeof(unsigned);
+  return (size_t)g.nrb * g.nslabs * kCounterStride * sizeof(unsigned);
 }
-size_t skinny_workspace_bytes(int64_t N, int64_t K, int split_k) {
-  const SkinnyGeom g = skinny_geom(N, K, split_k);
+size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int split_k) {
+  const SkinnyGeom g = skinny_geom(M, N, K, split_k);
   if (g.splits <= 1) return 0;
-  return (size_t)g.splits * g.nslabs * kMaxM * kSlab * sizeof(float);
+  return (size_t)g.splits * g.nrb * g.nslabs * kMaxM * kSlab * sizeof(float);
 }
-int64_t skinny_effective_splits(int64_t N, int64_t K, int split_k) { return skinny_geom(N, K, split_k).splits; }
+int64_t skinny_effective_splits(int64_t N, int64_t K, int split_k) { return skinny_geom(1, N, K, split_k).splits; }
 
 }  // namespace tilec

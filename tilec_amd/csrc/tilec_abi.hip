@@ -18,8 +18,8 @@ namespace tilec {
 const VariantDesc* skinny_variants(int* count);
 const VariantDesc* gemm_f32_variants(int* count);
 const VariantDesc* gemm_bf16_variants(int* count);
-size_t skinny_counter_bytes(int64_t N, int64_t K, int split_k);
-size_t skinny_workspace_bytes(int64_t N, int64_t K, int split_k);
+size_t skinny_counter_bytes(int64_t M, int64_t N, int64_t K, int split_k);
+size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int split_k);
 int64_t skinny_effective_splits(int64_t N, int64_t K, int split_k);
 }  // namespace tilec
 
@@ -62,18 +62,26 @@ constexpr int kCUs = 256;                               // MI355X compute units
 
 // The skinny kernel addresses x2 within one 16-row block with 32-bit byte
 // offsets (row * ldx2 * 4, row < 16, must stay < 2^31), and its split-K
-// partials with 32-bit offsets (splits * slabs * 4 KiB < 2^31).
+// partials with 32-bit offsets (splits * row blocks * slabs * 4 KiB < 2^31).
+// Row blocks of 16 are its grid's z dimension (at most 65535).
 constexpr int64_t kSkinnyMaxLdx1 = int64_t(1) << 25;
 constexpr int64_t kSkinnyMaxLdx2 = int64_t(1) << 25;
-constexpr int64_t kSkinnyMaxPartials = int64_t(1) << 19;  // splits * slabs
+constexpr int64_t kSkinnyMaxPartials = int64_t(1) << 19;  // splits * row blocks * slabs
+constexpr int64_t kSkinnyMaxRowBlocks = 65535;
 
 bool skinny_fits(int64_t ldx1, int64_t ldx2) { return ldx1 < kSkinnyMaxLdx1 && ldx2 < kSkinnyMaxLdx2; }
+
+// Output tiles of the smallest tile GEMM (64 x 64): below kCUs of them the
+// tile GEMMs cannot fill the chip and the streaming kernel, which splits K,
+// takes the product.
+bool small_output(int64_t M, int64_t N) { return cdiv(M, 64) * cdiv(N, 64) < kCUs; }
 
 // Built-in rule (used when the caller passes TILEC_VARIANT_AUTO).
 int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2) {
   (void)K;
   if (dtype == TILEC_F32) {
-    if (M <= 16 && skinny_fits(ldx1, ldx2)) return find("skinny_f32_w8_b1");
+    if ((M <= 16 || small_output(M, N)) && cdiv(M, 16) <= kSkinnyMaxRowBlocks && skinny_fits(ldx1, ldx2))
+      return find("skinny_f32_w8_b1");
     static const char* order[] = {"gemm_f32_256x256x16_w2x2", "gemm_f32_256x128x16_w2x2",
                                   "gemm_f32_128x128x16_w2x2", "gemm_f32_128x64x16_w2x2"};
     for (const char* nm : order) {
@@ -94,10 +102,10 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
 
 // split_k == 0 for the streaming kernel: enough workgroups for ~2 per CU,
 // while every wave still gets at least one full unrolled batch of rows.
-int auto_split(const VariantDesc* d, int64_t N, int64_t K) {
-  if (d->family != TILEC_FAMILY_SKINNY || N <= 0 || K <= 0) return 1;
-  const int64_t slabs = cdiv(N, d->bn);
-  int64_t s = cdiv(2 * kCUs, slabs);
+int auto_split(const VariantDesc* d, int64_t M, int64_t N, int64_t K) {
+  if (d->family != TILEC_FAMILY_SKINNY || M <= 0 || N <= 0 || K <= 0) return 1;
+  const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
+  int64_t s = cdiv(2 * kCUs, cells);
   const int64_t rows_per_split_min = 16LL * d->waves;  // one 16-row block per wave
   const int64_t s_max = K / rows_per_split_min;
   if (s > s_max) s = s_max;
@@ -130,16 +138,20 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
                 (long long)M);
   if (d->family == TILEC_FAMILY_SKINNY && !skinny_fits(ldx1 > 0 ? ldx1 : K, ldx2 > 0 ? ldx2 : N))
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s needs ldx1 < 2^25 and ldx2 < 2^25", d->name);
-  int s = split_k == 0 ? auto_split(d, N, K) : split_k;
+  int s = split_k == 0 ? auto_split(d, M, N, K) : split_k;
   if (d->family != TILEC_FAMILY_SKINNY && s != 1)
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s does not split K (split_k=%d)", d->name, s);
   if (d->family == TILEC_FAMILY_SKINNY) {
     const int64_t splits = skinny_effective_splits(N, K, s);
+    const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
+    if (cdiv(M, d->bm) > kSkinnyMaxRowBlocks)
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s takes M <= %lld (got %lld)", d->name,
+                  (long long)(kSkinnyMaxRowBlocks * d->bm), (long long)M);
     if (splits > 65535)
       return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
-    if (splits > 1 && splits * cdiv(N, d->bn) >= kSkinnyMaxPartials)
-      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits x %lld slabs of partials is too many",
-                  d->name, (long long)splits, (long long)cdiv(N, d->bn));
+    if (splits > 1 && splits * cells >= kSkinnyMaxPartials)
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits x %lld output blocks of partials is too many",
+                  d->name, (long long)splits, (long long)cells);
   }
   *out_d = d;
   *out_split = s;
@@ -167,11 +179,11 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
     if (ldx2 < N) return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < N=%lld", (long long)ldx2, (long long)N);
   }
   const bool skinny = d->family == TILEC_FAMILY_SKINNY;
-  const size_t need = skinny ? skinny_workspace_bytes(N, K, s) : 0;
+  const size_t need = skinny ? skinny_workspace_bytes(M, N, K, s) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu workspace bytes (got %zu)", d->name, need,
                 workspace == nullptr ? (size_t)0 : workspace_bytes);
-  const size_t need_cnt = skinny ? skinny_counter_bytes(N, K, s) : 0;
+  const size_t need_cnt = skinny ? skinny_counter_bytes(M, N, K, s) : 0;
   if (need_cnt > 0 && (counters == nullptr || counter_bytes < need_cnt))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu bytes of counters (got %zu)", d->name, need_cnt,
                 counters == nullptr ? (size_t)0 : counter_bytes);
@@ -203,7 +215,7 @@ size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t dty
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
   if (M == 0 || N == 0) return 0;
-  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(N, K, s) : 0;
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(M, N, K, s) : 0;
 }
 
 size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
@@ -212,7 +224,7 @@ size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
   if (M == 0 || N == 0) return 0;
-  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(N, K, s) : 0;
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(M, N, K, s) : 0;
 }
 
 int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {

@@ -74,14 +74,18 @@ _SKINNY_SPLITS = (1, 2, 4, 8, 16, 32, 64)
 def hip_configs(M, K, N, dtype="f32"):
     """Every (variant, split_k) the library can run for out[M,N] = x1[M,K]·x2[K,N].
 
-    The skinny family takes M <= 16 and a K split; the tile GEMMs take any M
-    and run unsplit.  This is the search space of tune.bench / tune.pick, as
-    `mm_configs` is for the reference's tuner (tilec/tune.py:82,148).
+    The skinny family (a K split, 16-row blocks) is offered for M <= 16 and
+    for outputs too small to fill the chip with 64x64 tiles; the tile GEMMs
+    take any M and run unsplit.  This is the search space of tune.bench /
+    tune.pick, as `mm_configs` is for the reference's tuner
+    (tilec/tune.py:82,148).
     """
     code = _dtype_code_name(dtype)
     out = []
     for v in _lib.variants():
         if v["dtype"] != code or (v["max_m"] and M > v["max_m"]):
+            continue
+        if v["family"] == _lib.FAMILY_SKINNY and not skinny_regime(M, N):
             continue
         if v["family"] == _lib.FAMILY_SKINNY:
             # A workgroup takes at most BK (the variant's K-slice cap) rows
@@ -97,6 +101,15 @@ def hip_configs(M, K, N, dtype="f32"):
         else:
             out.append((v["name"], 1))
     return out
+
+
+SMALL_OUTPUT_TILES = 256  # MI355X CUs: 64x64 output tiles below this leave CUs idle
+
+
+def skinny_regime(M, N):
+    """Whether the streaming (skinny) kernels are candidates: M <= 16, or
+    fewer 64x64 output tiles than CUs (the rule of tilec_select_variant)."""
+    return M <= 16 or cdiv(M, 64) * cdiv(N, 64) < SMALL_OUTPUT_TILES
 
 
 def _skinny_splits(K, split_k, kc_max):
