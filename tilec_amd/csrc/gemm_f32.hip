@@ -11,10 +11,14 @@
 //     next tile's global loads are issued before the current tile's MFMAs;
 //   * A stored k-major in LDS (As[k][m]) so every MFMA operand read is one
 //     conflict-free 32-bit LDS read per lane for both operands;
-//   * branch-free edges: clamped addresses plus selects on edge tiles and on
-//     the K tail only (the uniform per-tile test `interior` picks the unmasked
-//     path elsewhere), as the reference's if-converted masked loads do
-//     (README.md:50);
+//   * branch-free edges, as the reference's if-converted masked loads
+//     (README.md:50): with row strides that fit 32-bit offsets (BUF), every
+//     tile loads through buffer resources that end at the matrix's last
+//     element — rows past M (A) or K (B) get an out-of-range offset and load
+//     zeros, and when K or N is not a multiple of 4 a per-element select
+//     clears the columns past the edge of the quad that straddles it — so
+//     edge tiles cost what interior ones do; otherwise clamped addresses plus
+//     selects on edge tiles and the K tail;
 //   * XCD-aware, grouped tile order (tile_of in common.h).
 #include "common.h"
 #include "../../include/tilec.h"
@@ -59,7 +63,7 @@ __device__ __forceinline__ f32x4 ld4(const float* __restrict__ p, bool ok_all, i
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool VEC>
+template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t ldc, int group_m) {
@@ -81,8 +85,66 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
 
   f32x4 ra[P::A_Q], rb[P::B_Q];
 
+  // BUF: per-thread quad coordinates are fixed for the whole K loop; the
+  // resources move with k0.  Columns a quad keeps: A's K edge moves with the
+  // step, B's N edge is fixed per tile.
+  int a_row[P::A_Q], a_k[P::A_Q], b_k[P::B_Q], b_valid[P::B_Q];
+  uint32_t a_off[P::A_Q], b_off[P::B_Q];
+  if constexpr (BUF) {
+#pragma unroll
+    for (int p = 0; p < P::A_Q; ++p) {
+      const int e = tid + p * P::NT;
+      a_row[p] = e / (BK / 4);
+      a_k[p] = 4 * (e % (BK / 4));
+      a_off[p] = m0 + a_row[p] < M ? 4u * ((uint32_t)a_row[p] * (uint32_t)lda + (uint32_t)a_k[p]) : kOob;
+    }
+#pragma unroll
+    for (int p = 0; p < P::B_Q; ++p) {
+      const int e = tid + p * P::NT;
+      b_k[p] = e / (BN / 4);
+      const int n = 4 * (e % (BN / 4));
+      b_valid[p] = max(0, min(4, N - (n0 + n)));
+      b_off[p] = b_valid[p] > 0 ? 4u * ((uint32_t)b_k[p] * (uint32_t)ldb + (uint32_t)n) : kOob;
+    }
+  }
+  // Bytes from p to the end of a matrix of `rows` rows (row stride ld, last
+  // row `cols` long), clamped to a buffer's 31-bit range; 0 if none.
+  auto extent = [](int64_t rows_left, int64_t ld, int64_t cols_left) -> uint32_t {
+    if (rows_left <= 0 || cols_left <= 0) return 0u;
+    const int64_t bytes = 4 * ((rows_left - 1) * ld + cols_left);
+    return bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)bytes;
+  };
+  auto gload_buf = [&](int kt) {
+    const int k0 = kt * BK;
+    const BufRsrc rA = make_rsrc(A + (int64_t)m0 * lda + k0, extent(M - m0, lda, K - k0));
+    const BufRsrc rB = make_rsrc(B + (int64_t)k0 * ldb + n0, extent(K - k0, ldb, N - n0));
+#pragma unroll
+    for (int p = 0; p < P::A_Q; ++p) {
+      f32x4 v = load_f32x4(rA, k0 + a_k[p] < K ? a_off[p] : kOob);
+      if constexpr (!VEC) {
+        const int valid = K - (k0 + a_k[p]);
+#pragma unroll
+        for (int c = 1; c < 4; ++c) v[c] = c < valid ? v[c] : 0.f;
+      }
+      ra[p] = v;
+    }
+#pragma unroll
+    for (int p = 0; p < P::B_Q; ++p) {
+      f32x4 v = load_f32x4(rB, k0 + b_k[p] < K ? b_off[p] : kOob);
+      if constexpr (!VEC) {
+#pragma unroll
+        for (int c = 1; c < 4; ++c) v[c] = c < b_valid[p] ? v[c] : 0.f;
+      }
+      rb[p] = v;
+    }
+  };
+
   // Global -> registers for K tile kt.  MASK: clamp + select at every edge.
   auto gload = [&](int kt, bool mask) {
+    if constexpr (BUF) {
+      gload_buf(kt);
+      return;
+    }
     const int k0 = kt * BK;
 #pragma unroll
     for (int p = 0; p < P::A_Q; ++p) {
@@ -188,9 +250,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool VEC>
+template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF>
 hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
-  auto k = gemm_f32_kernel<BM, BN, BK, WM, WN, VEC>;
+  auto k = gemm_f32_kernel<BM, BN, BK, WM, WN, VEC, BUF>;
   const size_t lds = GemmF32<BM, BN, BK, WM, WN, VEC>::kLds;
   static bool attr_set = false;
   if (lds > 65536 && !attr_set) {
@@ -210,8 +272,13 @@ hipError_t launch_gemm_f32(const MatmulArgs& a) {
   if (tiles == 0) return hipSuccess;
   const bool vec = (a.K % 4 == 0) && (a.N % 4 == 0) && (a.ldx1 % 4 == 0) && (a.ldx2 % 4 == 0) &&
                    (reinterpret_cast<uintptr_t>(a.x1) % 16 == 0) && (reinterpret_cast<uintptr_t>(a.x2) % 16 == 0);
+  // Buffer offsets inside one K step: row * ld * 4 + 16 * quad < 2^31.
+  const bool buf = (int64_t)BM * a.ldx1 * 4 + 4 * BK < (int64_t(1) << 31) &&
+                   (int64_t)BK * a.ldx2 * 4 + 4 * BN < (int64_t(1) << 31);
   dim3 grid((unsigned)tiles);
-  return vec ? launch_one<BM, BN, BK, WM, WN, true>(a, grid) : launch_one<BM, BN, BK, WM, WN, false>(a, grid);
+  if (buf)
+    return vec ? launch_one<BM, BN, BK, WM, WN, true, true>(a, grid) : launch_one<BM, BN, BK, WM, WN, false, true>(a, grid);
+  return vec ? launch_one<BM, BN, BK, WM, WN, true, false>(a, grid) : launch_one<BM, BN, BK, WM, WN, false, false>(a, grid);
 }
 
 }  // namespace
