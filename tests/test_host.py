@@ -105,6 +105,23 @@ def test_tune_features_and_shapes():
     assert any(m <= 16 for m, _, _, _ in s) and any(d == "bf16" for *_, d in s)
 
 
+def test_tune_rotating_operands():
+    """Streaming-regime timings cycle x2 over copies that together exceed the
+    Infinity Cache (at most 16); tile-GEMM shapes and tiny x2 use x2 alone."""
+    import torch
+    x2 = torch.ones(1024, 1024)                      # 4 MiB
+    ops = tune.operands_for(1, 1024, 1024, x2)
+    assert len(ops) == 16 and ops[0] is x2 and all(o.data_ptr() != x2.data_ptr() for o in ops[1:])
+    assert all(torch.equal(o, x2) for o in ops)
+    big = torch.empty(8192, 8192, dtype=torch.bfloat16)   # 128 MiB: 4 copies reach 512 MiB
+    assert len(tune.operands_for(8, 8192, 8192, big)) == 4
+    ops = tune.operands_for(4096, 1024, 1024, x2)                   # 256 tiles: tile-GEMM regime
+    assert len(ops) == 1 and ops[0] is x2
+    small = torch.ones(64, 64)                                        # under 1 MiB
+    ops = tune.operands_for(1, 64, 64, small)
+    assert len(ops) == 1 and ops[0] is small
+
+
 def test_exported_trees_match_sklearn(tmp_path):
     from sklearn.ensemble import GradientBoostingRegressor
     rng = np.random.default_rng(0)
