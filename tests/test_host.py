@@ -143,6 +143,15 @@ def test_pick_returns_a_valid_config_or_none():
     assert tune.pick(0, 5, 5) is None
 
 
+def test_pick_uses_measured_best_for_benchmarked_shapes():
+    if not os.path.exists(tune.DATA) or not os.path.exists(tune.MODEL):
+        pytest.skip("no MI355X tuning data committed yet")
+    best = tune.best_table(tune.load())
+    for shape in tune.CONFIG_SHAPES:
+        want = tuple(best[",".join(map(str, shape))])
+        assert tune.pick(*shape) == want, shape
+
+
 def test_committed_tuning_data_schema():
     if not os.path.exists(tune.DATA):
         pytest.skip("no MI355X tuning data committed yet")

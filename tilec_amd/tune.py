@@ -15,7 +15,10 @@ What differs:
   * short calls are timed from replayed HIP graphs, and streaming-regime
     shapes cycle x2 over copies larger than the Infinity Cache;
   * the fitted trees are exported to JSON and evaluated here with numpy, so
-    `pick` needs neither scikit-learn nor a pickle at run time.
+    `pick` needs neither scikit-learn nor a pickle at run time;
+  * the export also carries the measured best config of every benchmarked
+    shape, which `pick` returns for those exact shapes (the model predicts
+    the rest).
 """
 
 import csv
@@ -272,12 +275,23 @@ def train(test_frac=0.2, seed=0, out=MODEL, path=None):
     print(f"model   : {report['model_geomean_vs_best']:.3f}x of best (geo mean), worst {report['model_worst_vs_best']:.2f}x")
     print(f"builtin : {report['builtin_geomean_vs_best']:.3f}x of best (geo mean), worst {report['builtin_worst_vs_best']:.2f}x")
     model = fit(rows)
-    export(model, out, report)
+    export(model, out, report, best_table(rows))
     return report
 
 
-def export(model, path, report=None):
-    """Write a fitted GradientBoostingRegressor as plain JSON trees."""
+def best_table(rows):
+    """Measured argmin per benchmarked shape: {"M,K,N,dtype": [kernel, split_k]}."""
+    best = {}
+    for r in rows:
+        k = _key(r)
+        if k not in best or r["ms"] < best[k]["ms"]:
+            best[k] = r
+    return {",".join(map(str, k)): [r["kernel"], int(r["split_k"])] for k, r in sorted(best.items())}
+
+
+def export(model, path, report=None, table=None):
+    """Write a fitted GradientBoostingRegressor as plain JSON trees, plus the
+    measured best config of every benchmarked shape (`table`)."""
     trees = []
     for est in model.estimators_[:, 0]:
         t = est.tree_
@@ -289,7 +303,8 @@ def export(model, path, report=None):
     init = float(model.init_.constant_[0][0]) if hasattr(model.init_, "constant_") else float(
         model._raw_predict_init([[0.0] * model.n_features_in_])[0][0])
     data = {"format": "gbr-trees-v1", "learning_rate": model.learning_rate, "init": init,
-            "n_features": int(model.n_features_in_), "trees": trees, "report": report or {}}
+            "n_features": int(model.n_features_in_), "trees": trees, "report": report or {},
+            "best": table or {}}
     with open(path, "w") as f:
         json.dump(data, f)
 
@@ -304,6 +319,8 @@ class TreeModel:
         self.n_features = data["n_features"]
         self.trees = [{k: np.asarray(t[k]) for k in ("left", "right", "feature", "threshold", "value")}
                       for t in data["trees"]]
+        self.best = {tuple(int(x) if i < 3 else x for i, x in enumerate(k.split(","))): tuple(v)
+                     for k, v in data.get("best", {}).items()}
 
     def predict(self, X):
         import numpy as np
@@ -335,7 +352,8 @@ def _model(path=MODEL):
 @lru_cache(4096)
 def pick(M, K, N, dtype="f32"):
     """(variant name, split_k) with the least predicted time, or None to use
-    the library's built-in rule (tilec/tune.py:143-151)."""
+    the library's built-in rule (tilec/tune.py:143-151).  A shape that was
+    benchmarked exactly takes its measured best config (when still offered)."""
     model = _model()
     if model is None or 0 in (M, K, N):
         return None
@@ -343,6 +361,9 @@ def pick(M, K, N, dtype="f32"):
     cands = ext.hip_configs(M, K, N, dtype)
     if not cands:
         return None
+    measured = model.best.get((M, K, N, dtype))
+    if measured is not None and measured in cands:
+        return measured
     cus = _cus()
     pred = model.predict([features(M, K, N, cus, dtype, k, s) for k, s in cands])
     return cands[int(pred.argmin())]
