@@ -80,7 +80,8 @@ def test_cpu_tensors_raise_not_fallback():
 def test_hip_configs_rules():
     names = {v["name"]: v for v in _lib.variants()}
     for M, K, N, dt in [(1, 4096, 4096, "f32"), (16, 4096, 4096, "f32"), (17, 4096, 4096, "f32"),
-                        (4096, 4096, 4096, "f32"), (8192, 8192, 8192, "bf16"), (3, 100, 7, "f32")]:
+                        (4096, 4096, 4096, "f32"), (8192, 8192, 8192, "bf16"), (3, 100, 7, "f32"),
+                        (1, 4096, 4096, "bf16"), (1024, 1024, 1024, "f32"), (520, 8192, 1648, "bf16")]:
         cfgs = ext.hip_configs(M, K, N, dt)
         assert cfgs and len(cfgs) == len(set(cfgs))
         for name, s in cfgs:
@@ -91,9 +92,36 @@ def test_hip_configs_rules():
                 eff = ext._skinny_splits(K, s, v["bk"])
                 assert eff == 1 or K // eff >= 16 * v["waves"]
             else:
-                assert s == 1
+                tiles = ext.cdiv(M, v["bm"]) * ext.cdiv(N, v["bn"])
+                eff = ext._gemm_splits(K, s, v["bk"])
+                assert eff == 1 or (ext.tile_can_split(v) and tiles < ext.SMALL_OUTPUT_TILES
+                                    and ext.cdiv(K, v["bk"]) >= 4 * eff)
         has_skinny = any(names[n]["family"] == _lib.FAMILY_SKINNY for n, _ in cfgs)
         assert has_skinny == (ext.skinny_regime(M, N) and dt == "f32")
+    # Few tiles: the tile GEMMs that can split are offered split configs.
+    assert ("gemm_bf16_128x128x64_r4", 8) in ext.hip_configs(1, 4096, 4096, "bf16")
+    assert ("gemm_f32_128x64x16_w2x2", 4) in ext.hip_configs(1024, 1024, 1024, "f32")
+    assert all(s == 1 for _, s in ext.hip_configs(8192, 8192, 8192, "bf16"))
+
+
+def test_gemm_split_geometry_matches_the_library():
+    """Workspace the C ABI asks for a split tile GEMM = splits * tiles *
+    BM * BN floats; counters = one 256-byte line per tile; unsplittable
+    tiles are refused."""
+    L = _lib.lib()
+    v = _lib.variants()[_lib.variant_id("gemm_f32_64x64x16_w2x2")]
+    for M, N, K, s in [(1024, 1024, 1024, 4), (100, 70, 1000, 3), (64, 64, 4096, 16), (64, 64, 40, 8)]:
+        eff = ext._gemm_splits(K, s, v["bk"])
+        tiles = ext.cdiv(M, 64) * ext.cdiv(N, 64)
+        ws = L.tilec_matmul_workspace_bytes(M, N, K, _lib.F32, v["id"], s)
+        cnt = L.tilec_matmul_counter_bytes(M, N, K, _lib.F32, v["id"], s)
+        assert ws == (eff * tiles * 64 * 64 * 4 if eff > 1 else 0), (M, N, K, s)
+        assert cnt == (tiles * 256 if eff > 1 else 0)
+    big = _lib.variant_id("gemm_bf16_256x256x64_r2")
+    assert _call(M=256, N=256, K=4096, dtype=_lib.BF16, variant=big, split=4) == _lib.ERR_UNSUPPORTED
+    assert L.tilec_auto_split_k(256, 256, 4096, _lib.BF16, big) == 1
+    small = _lib.variant_id("gemm_bf16_128x128x64_r4")
+    assert L.tilec_auto_split_k(1, 4096, 4096, _lib.BF16, small) > 1
 
 
 def test_tune_features_and_shapes():
@@ -220,7 +248,9 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert _call(M=16 * 65535 + 1, variant=skinny) == _lib.ERR_UNSUPPORTED
     assert "M <=" in _lib.last_error()
     assert _call(variant=bf16, dtype=0) == _lib.ERR_UNSUPPORTED
-    assert _call(variant=gemm, split=2) == _lib.ERR_UNSUPPORTED
+    # Tile GEMMs split K (workspace required) unless a thread's tile is too big to.
+    assert _call(M=64, N=64, K=4096, variant=gemm, split=2) == _lib.ERR_WORKSPACE
+    assert _call(K=4096, variant=_lib.variant_id("gemm_f32_256x256x16_w2x2"), split=2) == _lib.ERR_UNSUPPORTED
     # Split K needs a workspace.
     assert _call(M=4, N=256, K=4096, variant=skinny, split=4) == _lib.ERR_WORKSPACE
     assert "workspace" in _lib.last_error()
@@ -263,7 +293,10 @@ def test_workspace_geometry():
     assert L.tilec_matmul_workspace_bytes(16, 4096, 4096, 0, _lib.variant_id("gemm_f32_128x128x16_w2x2"), 1) == 0
     s = L.tilec_auto_split_k(16, 4096, 4096, 0, v)
     assert 1 <= s <= 4096 // (4 * 8 * 4)
-    assert L.tilec_auto_split_k(16, 4096, 4096, 0, _lib.variant_id("gemm_f32_128x128x16_w2x2")) == 1
+    # tile GEMMs: 32 tiles of 128 x 128 split K to fill the CUs; 1024 tiles do not split
+    g = _lib.variant_id("gemm_f32_128x128x16_w2x2")
+    assert L.tilec_auto_split_k(16, 4096, 4096, 0, g) == 8
+    assert L.tilec_auto_split_k(4096, 4096, 4096, 0, g) == 1
 
 
 def test_select_variant_rules():

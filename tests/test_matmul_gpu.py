@@ -122,6 +122,46 @@ def test_bf16_variant_ragged(name):
         assert O.rel_l2(got, O.matmul_bf16_f64(a16, b16)) <= 1e-5, (name, (m, k, n))
 
 
+def _splittable(dtype_code):
+    return [v["name"] for v in _lib.variants()
+            if v["family"] == _lib.FAMILY_GEMM and v["dtype"] == dtype_code and ext.tile_can_split(v)]
+
+
+SPLIT_SHAPES = [(1, 1000, 65), (17, 4097, 33), (64, 1024, 64), (127, 1000, 513), (200, 3001, 129), (520, 2048, 300)]
+
+
+@pytest.mark.parametrize("name", _splittable(_lib.F32) + _splittable(_lib.BF16))
+def test_gemm_split_k(name):
+    """K split across workgroups of a tile GEMM: partial tiles combined by the
+    last split in split order — oracle parity, bit-exact integers, and the
+    same bits on a repeat call."""
+    v = _lib.variants()[_lib.variant_id(name)]
+    bf16 = v["dtype"] == _lib.BF16
+    for i, (m, k, n) in enumerate(SPLIT_SHAPES):
+        if bf16:
+            a16 = O.bf16_round(O.normal((m, k), 700 + 2 * i))
+            b16 = O.bf16_round(O.normal((k, n), 701 + 2 * i))
+            x1, x2, ref, tol = dev_bf16(a16), dev_bf16(b16), O.matmul_bf16_f64(a16, b16), 1e-5
+        else:
+            a, b = O.normal((m, k), 700 + 2 * i), O.normal((k, n), 701 + 2 * i)
+            x1, x2, ref, tol = dev(a), dev(b), O.matmul_f64(a, b), O.TOL_F32
+        for s in (2, 3, 8):
+            say(f"{name} split {s} shape {(m, k, n)}")
+            got = run(x1, x2, (name, s))
+            assert O.rel_l2(got, ref) <= tol, (name, s, (m, k, n))
+            np.testing.assert_array_equal(run(x1, x2, (name, s)), got)
+    rng = np.random.default_rng(5)
+    a = rng.integers(-3, 4, (70, 1500)).astype(np.float32)
+    b = rng.integers(-3, 4, (1500, 90)).astype(np.float32)
+    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    if bf16:
+        x1, x2 = dev(a).to(torch.bfloat16), dev(b).to(torch.bfloat16)  # small integers are exact in bf16
+    else:
+        x1, x2 = dev(a), dev(b)
+    for s in (1, 4, 7):
+        np.testing.assert_array_equal(run(x1, x2, (name, s)), want)
+
+
 def test_skinny_shapes_and_splits():
     for m in (1, 2, 4, 7, 15, 16):
         for k, n in [(1, 1), (5, 63), (1000, 65), (4096, 130), (4097, 4096)]:

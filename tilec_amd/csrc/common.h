@@ -98,6 +98,129 @@ __device__ __forceinline__ void store_f32x4_coherent(BufRsrc r, uint32_t off, f3
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------------------
+// Split-K combine for tile kernels (grid y = K splits).  Every workgroup of
+// a tile holds its partial sums as NV f32x4 per thread.  It publishes them to
+// `ws` in a per-thread layout — value v of thread t of split s of tile `tile`
+// at float4 index ((s * tiles + tile) * NV + v) * NT + t, so each store and
+// load instruction is contiguous across the workgroup — waits for the stores
+// to complete, and counts itself in on the tile's counter (its own 256-byte
+// line).  The workgroup that brings the count to S resets the counter, adds
+// the S partials in split order (its own from registers), leaves the sums in
+// `v` and returns true; the others return false.  The order of additions
+// depends only on S, so results are deterministic.  Coherence across XCDs
+// without cache-wide fences: agent-coherent (sc1) data accesses, waits before
+// the barrier, a relaxed agent-scope atomic for the count.  The host keeps
+// S * tiles * NV * NT * 16 bytes below 2^31.
+// ---------------------------------------------------------------------------
+constexpr int kSplitCounterStride = 64;  // uint32s between tile counters
+// Tile kernels split K only when a thread holds at most this many fp32
+// accumulators: the combine keeps them, their sum and a batch of loads in
+// registers (larger tiles would spill, and have enough tiles not to need it).
+constexpr int kSplitMaxAccPerThread = 64;
+__host__ __device__ constexpr bool tile_can_split(int bm, int bn, int waves) {
+  return bm * bn <= kSplitMaxAccPerThread * 64 * waves;
+}
+
+template <int NT, int NV>
+__device__ __forceinline__ bool splitk_combine(f32x4 (&v)[NV], int split, int S, int tile, int tiles,
+                                               float* __restrict__ ws, unsigned* __restrict__ counters,
+                                               int* last_flag) {
+  const uint32_t tid = threadIdx.x;
+  const BufRsrc rw = make_rsrc(ws);
+  auto off = [&](int s, int q) { return 16u * ((uint32_t)((s * tiles + tile) * NV + q) * NT + tid); };
+#pragma unroll
+  for (int q = 0; q < NV; ++q) store_f32x4_coherent(rw, off(split, q), v[q]);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid < 64) {
+    unsigned prev = 0;
+    if (tid == 0)
+      prev = __hip_atomic_fetch_add(&counters[tile * kSplitCounterStride], 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    prev = (unsigned)__shfl((int)prev, 0);
+    if (tid == 0) *last_flag = prev == (unsigned)(S - 1);
+  }
+  __syncthreads();
+  if (!*last_flag) return false;
+  if (tid == 0)
+    __hip_atomic_store(&counters[tile * kSplitCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // CH splits per round of loads (at most 16 float4 in flight per thread).
+  constexpr int CH = NV >= 16 ? 1 : 16 / NV;
+  f32x4 t[NV];
+#pragma unroll
+  for (int q = 0; q < NV; ++q) t[q] = v[q];  // placeholder; overwritten by split 0 below
+  for (int s0 = 0; s0 < S; s0 += CH) {
+    f32x4 p[CH][NV];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int s = s0 + j;
+      const bool load = s < S && s != split;
+#pragma unroll
+      for (int q = 0; q < NV; ++q) p[j][q] = load_f32x4_coherent(rw, load ? off(s, q) : kOob);
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int s = s0 + j;
+      if (s >= S) break;
+#pragma unroll
+      for (int q = 0; q < NV; ++q) {
+        const f32x4 x = s == split ? v[q] : p[j][q];
+        t[q] = s == 0 ? x : t[q] + x;
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NV; ++q) v[q] = t[q];
+  return true;
+}
+
+// splitk_combine for the TM x TN blocks of 32x32 MFMA accumulators of the
+// tile kernels: true (with the summed tile in acc) in the last split only.
+template <int TM, int TN, int NT>
+__device__ __forceinline__ bool splitk_tile(f32x16 (&acc)[TM][TN], int split, int S, int tile, int tiles,
+                                            float* __restrict__ ws, unsigned* __restrict__ counters,
+                                            int* last_flag) {
+  constexpr int NV = TM * TN * 4;
+  if constexpr (TM * TN * 16 > kSplitMaxAccPerThread) {
+    return true;  // never split (the host passes S == 1 for these tiles)
+  } else {
+  f32x4 v[NV];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v[(i * TN + j) * 4 + q] =
+            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+  if (!splitk_combine<NT, NV>(v, split, S, tile, tiles, ws, counters, last_flag)) return false;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[i][j][4 * q + c] = v[(i * TN + j) * 4 + q][c];
+  return true;
+  }
+}
+
+// K splits of a tile kernel: `steps` K steps of BK per split (the last may
+// be shorter), `splits` = how many are non-empty.  K == 0: one empty split.
+struct SplitGeom {
+  int64_t splits, steps;
+};
+inline SplitGeom gemm_split_geom(int64_t K, int64_t BK, int split_k) {
+  const int64_t total = cdiv(K, BK);
+  if (total <= 0) return {1, 0};
+  int64_t s = split_k < 1 ? 1 : split_k;
+  if (s > total) s = total;
+  const int64_t steps = cdiv(total, s);
+  return {cdiv(total, steps), steps};
+}
+
+// ---------------------------------------------------------------------------
 // Workgroup id -> output tile.
 // The dispatcher hands workgroups to the 8 XCDs round-robin (id i runs on
 // XCD i % 8) and every XCD has its own L2.  First renumber ids so that each

@@ -55,9 +55,11 @@ __device__ __forceinline__ u16x8 ld8(const u16* __restrict__ p, bool ok_all, int
 template <int BM, int BN, int BK, int WM, int WN, bool VEC>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
     const u16* __restrict__ A, const u16* __restrict__ B, float* __restrict__ C, int M, int N, int K,
-    int64_t lda, int64_t ldb, int64_t ldc, int group_m) {
+    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
+    unsigned* __restrict__ counters) {
   using P = GemmBf16<BM, BN, BK, WM, WN>;
   extern __shared__ __align__(16) u16 lds_u16[];
+  __shared__ int last_flag;
   u16* As = lds_u16;                          // [2][BM][LDS_K]
   u16* Bs = lds_u16 + 2 * BM * P::LDS_K;      // [2][BN][LDS_K]
 
@@ -69,7 +71,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
   tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
-  const int nk = (K + BK - 1) / BK;
+  // K steps [kt0, kt1) of this workgroup (grid y = K splits).
+  const int split = blockIdx.y, S = gridDim.y;
+  const int kt0 = split * split_steps;
+  const int kt1 = min((K + BK - 1) / BK, kt0 + split_steps);
   const int nk_full = K / BK;
 
   u16x8 ra[P::A_Q], rb[P::B_Q];
@@ -130,8 +135,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  if (nk > 0) {
-    gload(0, !(interior && nk_full > 0));
+  if (kt0 < kt1) {
+    gload(kt0, !(interior && kt0 < nk_full));
     sstore(0);
     __syncthreads();
   }
@@ -140,9 +145,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
   const int bcol = wn * P::WTN + (lane & 31);
   const int khalf = lane >> 5;
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nk;
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int buf = (kt - kt0) & 1;
+    const bool more = kt + 1 < kt1;
     if (more) gload(kt + 1, !(interior && kt + 1 < nk_full));
     const u16* as = As + buf * BM * P::LDS_K;
     const u16* bs = Bs + buf * BN * P::LDS_K;
@@ -165,6 +170,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
     __syncthreads();
   }
 
+  if (S > 1 && !splitk_tile<P::TM, P::TN, P::NT>(acc, split, S, blockIdx.x, gridDim.x, ws, counters, &last_flag))
+    return;
+
   const int row_base = m0 + wm * P::WTM + 4 * khalf;
   const int col_base = n0 + bcol;
 #pragma unroll
@@ -182,7 +190,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
 
 template <int BM, int BN, int BK, int WM, int WN, bool VEC>
 hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
+  using P = GemmBf16<BM, BN, BK, WM, WN>;
   auto k = gemm_bf16_kernel<BM, BN, BK, WM, WN, VEC>;
+  const SplitGeom g = gemm_split_geom(a.K, BK, a.split_k);
+  if (g.splits > 1 && P::TM * P::TN * 16 > kSplitMaxAccPerThread) return hipErrorInvalidConfiguration;
+  grid.y = (unsigned)g.splits;
   const size_t lds = GemmBf16<BM, BN, BK, WM, WN>::kLds;
   static bool attr_set = false;
   if (lds > 65536 && !attr_set) {
@@ -192,7 +204,7 @@ hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
   }
   hipLaunchKernelGGL(k, grid, dim3(WM * WN * 64), lds, a.stream, static_cast<const u16*>(a.x1),
                      static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo,
-                     8);
+                     8, (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr, g.splits > 1 ? a.counters : nullptr);
   return hipGetLastError();
 }
 
@@ -205,9 +217,10 @@ namespace {
 
 // Aligned operands (16-byte base, K, N, lda, ldb multiples of 8) whose tile
 // offsets fit 32 bits run the LDS-DMA kernel of gemm_bf16_lds.hip with a
-// ring of NBUF stage buffers of BK and WM x WN waves; everything else runs
-// the generic kernel above (2 x 2 waves) with the same output tile
-// (NBUF == 0: generic kernel only).
+// ring of NBUF stage buffers of BK; everything else runs the generic kernel
+// above with the same output tile (NBUF == 0: generic kernel only).  Both
+// use the variant's WM x WN waves, so a K split is possible in one exactly
+// when it is in the other.
 template <int BM, int BN, int BK, int NBUF, int WM = 2, int WN = 2>
 hipError_t launch_gemm_bf16(const MatmulArgs& a) {
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
@@ -219,7 +232,7 @@ hipError_t launch_gemm_bf16(const MatmulArgs& a) {
       return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN>(a);
   }
   dim3 grid((unsigned)tiles);
-  return vec ? launch_one<BM, BN, 64, 2, 2, true>(a, grid) : launch_one<BM, BN, 64, 2, 2, false>(a, grid);
+  return vec ? launch_one<BM, BN, 64, WM, WN, true>(a, grid) : launch_one<BM, BN, 64, WM, WN, false>(a, grid);
 }
 
 }  // namespace

@@ -95,9 +95,11 @@ __device__ __forceinline__ void sched_mfma_vmem() {
 template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool KFULL>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     const u16* __restrict__ A, const u16* __restrict__ B, float* __restrict__ C, int M, int N, int K,
-    int64_t lda, int64_t ldb, int64_t ldc, int group_m) {
+    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
+    unsigned* __restrict__ counters) {
   using P = LdsGemm<BM, BN, BK, NBUF, WM, WN>;
   constexpr int KS = BK / 16;  // MFMA k-slices per step
+  __shared__ int last_flag;
   // The ring: distinct LDS objects (those past NBUF are never referenced).
   __shared__ __align__(16) char lds0[P::STAGE_BYTES];
   __shared__ __align__(16) char lds1[P::STAGE_BYTES];
@@ -119,49 +121,62 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int nk = (K + BK - 1) / BK;
+  // This workgroup's K steps: [kt0, kt0 + nk) of the cdiv(K, BK) steps
+  // (grid y = K splits of split_steps steps each; one split = all of K).
+  const int split = blockIdx.y, S = gridDim.y;
+  const int kt0 = split * split_steps;
+  const int nk = max(0, min((K + BK - 1) / BK, kt0 + split_steps) - kt0);
 
-  // ---- global -> LDS for K step kt ---------------------------------------
+  // ---- global -> LDS for K step kt (local: absolute step kt0 + kt) ----------
   // Physical chunk p of the A stage holds row p / A_ROW_CHUNKS, logical chunk
   // (p % A_ROW_CHUNKS) ^ swz_a(row); of the B stage, k-row p / B_ROW_CHUNKS,
   // logical chunk (p % B_ROW_CHUNKS) ^ swz_b(row).  Instruction i of this
   // wave fills physical chunks [64 * (wave * INSTR + i), +64), lane l the
   // l-th of them.  A lane's byte offset from the step's base is the same in
-  // every step; rows past M and columns past N get kOob once, here.  When
-  // K % BK == 0 (KFULL) no other mask is needed and a step past K gets a
-  // resource of zero records, so its loads touch nothing; otherwise the
-  // k-bounds are checked per step.
+  // every step; rows past M and columns past N get kOob once, here.  A step
+  // past this workgroup's range gets a resource of zero records, so its
+  // loads touch nothing.  When K % BK != 0 (!KFULL) the last step also masks
+  // A's chunks past K per lane and B's rows past K by the resource's size.
   uint32_t off_a[P::A_INSTR], off_b[P::B_INSTR];
-  int krow_b[P::B_INSTR], kcol_a[P::A_INSTR];
+  // Column within the A stage of this lane's chunk of instruction i;
+  // recomputed where needed rather than held in registers.
+  auto dma_a_kcol = [&](int i) {
+    const int p = 64 * (wave * P::A_INSTR + i) + lane;
+    const int row = p / P::A_ROW_CHUNKS;
+    return 8 * ((p % P::A_ROW_CHUNKS) ^ swz_a<BK>(row));
+  };
 #pragma unroll
   for (int i = 0; i < P::A_INSTR; ++i) {
     const int p = 64 * (wave * P::A_INSTR + i) + lane;
-    const int row = p / P::A_ROW_CHUNKS, c = (p % P::A_ROW_CHUNKS) ^ swz_a<BK>(row);
-    kcol_a[i] = 8 * c;
-    off_a[i] = m0 + row < M ? 2u * ((uint32_t)row * (uint32_t)lda + 8u * c) : kOob;
+    const int row = p / P::A_ROW_CHUNKS;
+    off_a[i] = m0 + row < M ? 2u * ((uint32_t)row * (uint32_t)lda + (uint32_t)dma_a_kcol(i)) : kOob;
   }
 #pragma unroll
   for (int i = 0; i < P::B_INSTR; ++i) {
     const int p = 64 * (wave * P::B_INSTR + i) + lane;
     const int row = p / P::B_ROW_CHUNKS, c = (p % P::B_ROW_CHUNKS) ^ swz_b(row);
-    krow_b[i] = row;
     off_b[i] = n0 + 8 * c < N ? 2u * ((uint32_t)row * (uint32_t)ldb + 8u * c) : kOob;
   }
   // Instruction q (0 <= q < IPS) of step kt: A instructions first, then B.
   auto dma_one = [&](int q, int kt, char* st) __attribute__((always_inline)) {
-    const int k0 = kt * BK;
+    const int k0 = (kt0 + kt) * BK;
     const uint32_t recs = kt < nk ? 0x7FFFFFFFu : 0u;
     if (q < P::A_INSTR) {
       const BufRsrc ra = make_rsrc(A + (int64_t)m0 * lda + k0, recs);
       uint32_t off = off_a[q];
-      if constexpr (!KFULL) off = k0 + kcol_a[q] < K ? off : kOob;
+      if constexpr (!KFULL) off = k0 + dma_a_kcol(q) < K ? off : kOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + 16 * 64 * (wave * P::A_INSTR + q)), 16, off, 0,
                                                0, 0);
     } else {
       const int i = q - P::A_INSTR;
-      const BufRsrc rb = make_rsrc(B + (int64_t)k0 * ldb + n0, recs);
-      uint32_t off = off_b[i];
-      if constexpr (!KFULL) off = k0 + krow_b[i] < K ? off : kOob;
+      // B's K edge is the end of whole rows: a resource of (K - k0) rows
+      // masks the rows past it without a per-lane test.
+      uint32_t recs_b = recs;
+      if constexpr (!KFULL) recs_b = kt < nk ? (uint32_t)min<int64_t>((int64_t)(K - k0) * ldb * 2, 0x7FFFFFFF) : 0u;
+      const BufRsrc rb = make_rsrc(B + (int64_t)k0 * ldb + n0, recs_b);
+      // (a copy, not the array element itself: passed straight to the
+      // builtin, the element makes the host pass drop the kernel's stub)
+      const uint32_t off = off_b[i];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(st + P::A_BYTES + 16 * 64 * (wave * P::B_INSTR + i)),
                                                16, off, 0, 0, 0);
     }
@@ -303,6 +318,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   // land before this workgroup can finish and release its LDS.
   __builtin_amdgcn_s_waitcnt(0);
 
+  // Split K: publish this workgroup's partial tile; the last of the tile's
+  // splits adds them in split order and writes C.
+  if (S > 1 && !splitk_tile<P::TM, P::TN, P::NT>(acc, split, S, blockIdx.x, gridDim.x, ws, counters, &last_flag))
+    return;
+
   // Epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each block.
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
   const int row_base = m0 + wm * P::WTM + 4 * h;
@@ -329,10 +349,14 @@ hipError_t launch_gemm_bf16_lds(const MatmulArgs& a) {
   using P = LdsGemm<BM, BN, BK, NBUF, WM, WN>;
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
   if (tiles == 0) return hipSuccess;
+  const SplitGeom g = gemm_split_geom(a.K, BK, a.split_k);
+  if (g.splits > 1 && P::TM * P::TN * 16 > kSplitMaxAccPerThread) return hipErrorInvalidConfiguration;
   auto kern = a.K % BK == 0 ? gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, true>
                             : gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, false>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(P::NT), 0, a.stream, static_cast<const u16*>(a.x1),
-                     static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo, 4);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)g.splits), dim3(P::NT), 0, a.stream,
+                     static_cast<const u16*>(a.x1), static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N,
+                     (int)a.K, a.ldx1, a.ldx2, a.ldo, 4, (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr,
+                     g.splits > 1 ? a.counters : nullptr);
   return hipGetLastError();
 }
 

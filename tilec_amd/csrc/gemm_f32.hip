@@ -66,9 +66,11 @@ __device__ __forceinline__ f32x4 ld4(const float* __restrict__ p, bool ok_all, i
 template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
-    int64_t lda, int64_t ldb, int64_t ldc, int group_m) {
+    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
+    unsigned* __restrict__ counters) {
   using P = GemmF32<BM, BN, BK, WM, WN, VEC>;
   extern __shared__ __align__(16) float lds[];
+  __shared__ int last_flag;
   float* As = lds;                          // [2][BK][LDA_S]
   float* Bs = lds + 2 * BK * P::LDA_S;      // [2][BK][LDB_S]
 
@@ -80,7 +82,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
   tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
-  const int nk = (K + BK - 1) / BK;
+  // K steps [kt0, kt1) of this workgroup (grid y = K splits).
+  const int split = blockIdx.y, S = gridDim.y;
+  const int kt0 = split * split_steps;
+  const int kt1 = min((K + BK - 1) / BK, kt0 + split_steps);
   const int nk_full = K / BK;
 
   f32x4 ra[P::A_Q], rb[P::B_Q];
@@ -201,8 +206,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  if (nk > 0) {
-    gload(0, !(interior && nk_full > 0));
+  if (kt0 < kt1) {
+    gload(kt0, !(interior && kt0 < nk_full));
     sstore(0);
     __syncthreads();
   }
@@ -211,9 +216,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
   const int bcol = wn * P::WTN + (lane & 31);
   const int khalf = lane >> 5;
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nk;
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int buf = (kt - kt0) & 1;
+    const bool more = kt + 1 < kt1;
     if (more) gload(kt + 1, !(interior && kt + 1 < nk_full));
     const float* as = As + buf * BK * P::LDA_S;
     const float* bs = Bs + buf * BK * P::LDB_S;
@@ -234,6 +239,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     __syncthreads();
   }
 
+  if (S > 1 && !splitk_tile<P::TM, P::TN, P::NT>(acc, split, S, blockIdx.x, gridDim.x, ws, counters, &last_flag))
+    return;
+
   // Epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each block.
   const int row_base = m0 + wm * P::WTM + 4 * khalf;
   const int col_base = n0 + bcol;
@@ -252,7 +260,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
 
 template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF>
 hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
+  using P = GemmF32<BM, BN, BK, WM, WN, VEC>;
   auto k = gemm_f32_kernel<BM, BN, BK, WM, WN, VEC, BUF>;
+  const SplitGeom g = gemm_split_geom(a.K, BK, a.split_k);
+  if (g.splits > 1 && P::TM * P::TN * 16 > kSplitMaxAccPerThread) return hipErrorInvalidConfiguration;
+  grid.y = (unsigned)g.splits;
   const size_t lds = GemmF32<BM, BN, BK, WM, WN, VEC>::kLds;
   static bool attr_set = false;
   if (lds > 65536 && !attr_set) {
@@ -262,7 +274,7 @@ hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
   }
   hipLaunchKernelGGL(k, grid, dim3(WM * WN * 64), lds, a.stream, static_cast<const float*>(a.x1),
                      static_cast<const float*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo,
-                     8);
+                     8, (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr, g.splits > 1 ? a.counters : nullptr);
   return hipGetLastError();
 }
 

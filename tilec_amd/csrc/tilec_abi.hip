@@ -76,6 +76,22 @@ bool skinny_fits(int64_t ldx1, int64_t ldx2) { return ldx1 < kSkinnyMaxLdx1 && l
 // takes the product.
 bool small_output(int64_t M, int64_t N) { return cdiv(M, 64) * cdiv(N, 64) < kCUs; }
 
+// Tile-GEMM split-K partials are addressed with 32-bit byte offsets
+// (splits * tiles * BM * BN * 4 < 2^31) and splits are grid y (<= 65535).
+constexpr int64_t kGemmMaxPartialBytes = (int64_t(1) << 31) - 1;
+
+int64_t gemm_tiles(const VariantDesc* d, int64_t M, int64_t N) { return cdiv(M, d->bm) * cdiv(N, d->bn); }
+
+size_t gemm_workspace_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K, int s) {
+  const SplitGeom g = gemm_split_geom(K, d->bk, s);
+  if (g.splits <= 1) return 0;
+  return (size_t)g.splits * gemm_tiles(d, M, N) * d->bm * d->bn * sizeof(float);
+}
+size_t gemm_counter_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K, int s) {
+  if (gemm_split_geom(K, d->bk, s).splits <= 1) return 0;
+  return (size_t)gemm_tiles(d, M, N) * kSplitCounterStride * sizeof(unsigned);
+}
+
 // Built-in rule (used when the caller passes TILEC_VARIANT_AUTO).
 int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2) {
   (void)K;
@@ -97,13 +113,25 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
     const VariantDesc* d = table()[v];
     if (cdiv(M, d->bm) * cdiv(N, d->bn) >= kCUs) return v;
   }
-  return find("gemm_bf16_64x64x64_w2x2");
+  // Few output tiles: the 128 x 128 LDS kernel, with K split to fill the chip.
+  return find("gemm_bf16_128x128x64_r4");
 }
 
-// split_k == 0 for the streaming kernel: enough workgroups for ~2 per CU,
-// while every wave still gets at least one full unrolled batch of rows.
+// split_k == 0.  Streaming kernel: enough workgroups for ~2 per CU, while
+// every wave still gets at least one full unrolled batch of rows.  Tile
+// GEMMs: unsplit when the tiles alone fill the CUs, else about one workgroup
+// per CU, keeping at least 4 K steps per split (at most 16 splits).
 int auto_split(const VariantDesc* d, int64_t M, int64_t N, int64_t K) {
-  if (d->family != TILEC_FAMILY_SKINNY || M <= 0 || N <= 0 || K <= 0) return 1;
+  if (M <= 0 || N <= 0 || K <= 0) return 1;
+  if (d->family == TILEC_FAMILY_GEMM) {
+    const int64_t tiles = gemm_tiles(d, M, N);
+    if (tiles >= kCUs || !tile_can_split(d->bm, d->bn, d->waves)) return 1;
+    int64_t s = cdiv(kCUs, tiles);
+    const int64_t s_max = cdiv(K, d->bk) / 4;
+    if (s > s_max) s = s_max;
+    if (s > 16) s = 16;
+    return s < 1 ? 1 : (int)s;
+  }
   const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
   int64_t s = cdiv(2 * kCUs, cells);
   const int64_t rows_per_split_min = 16LL * d->waves;  // one 16-row block per wave
@@ -139,8 +167,16 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
   if (d->family == TILEC_FAMILY_SKINNY && !skinny_fits(ldx1 > 0 ? ldx1 : K, ldx2 > 0 ? ldx2 : N))
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s needs ldx1 < 2^25 and ldx2 < 2^25", d->name);
   int s = split_k == 0 ? auto_split(d, M, N, K) : split_k;
-  if (d->family != TILEC_FAMILY_SKINNY && s != 1)
-    return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s does not split K (split_k=%d)", d->name, s);
+  if (d->family == TILEC_FAMILY_GEMM) {
+    const SplitGeom g = gemm_split_geom(K, d->bk, s);
+    if (g.splits > 1 && !tile_can_split(d->bm, d->bn, d->waves))
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s does not split K (split_k=%d)", d->name, s);
+    if (g.splits > 65535)
+      return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
+    if (g.splits > 1 && (int64_t)gemm_workspace_bytes(d, M, N, K, s) > kGemmMaxPartialBytes)
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits of %lld tiles of partials is too many", d->name,
+                  (long long)g.splits, (long long)gemm_tiles(d, M, N));
+  }
   if (d->family == TILEC_FAMILY_SKINNY) {
     const int64_t splits = skinny_effective_splits(N, K, s);
     const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
@@ -179,11 +215,11 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
     if (ldx2 < N) return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < N=%lld", (long long)ldx2, (long long)N);
   }
   const bool skinny = d->family == TILEC_FAMILY_SKINNY;
-  const size_t need = skinny ? skinny_workspace_bytes(M, N, K, s) : 0;
+  const size_t need = skinny ? skinny_workspace_bytes(M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu workspace bytes (got %zu)", d->name, need,
                 workspace == nullptr ? (size_t)0 : workspace_bytes);
-  const size_t need_cnt = skinny ? skinny_counter_bytes(M, N, K, s) : 0;
+  const size_t need_cnt = skinny ? skinny_counter_bytes(M, N, K, s) : gemm_counter_bytes(d, M, N, K, s);
   if (need_cnt > 0 && (counters == nullptr || counter_bytes < need_cnt))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu bytes of counters (got %zu)", d->name, need_cnt,
                 counters == nullptr ? (size_t)0 : counter_bytes);
@@ -215,7 +251,7 @@ size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t dty
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
   if (M == 0 || N == 0) return 0;
-  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(M, N, K, s) : 0;
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
 }
 
 size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
@@ -224,7 +260,7 @@ size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
   if (M == 0 || N == 0) return 0;
-  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(M, N, K, s) : 0;
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(M, N, K, s) : gemm_counter_bytes(d, M, N, K, s);
 }
 
 int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {

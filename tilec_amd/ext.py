@@ -76,9 +76,10 @@ def hip_configs(M, K, N, dtype="f32"):
 
     The skinny family (a K split, 16-row blocks) is offered for M <= 16 and
     for outputs too small to fill the chip with 64x64 tiles; the tile GEMMs
-    take any M and run unsplit.  This is the search space of tune.bench /
-    tune.pick, as `mm_configs` is for the reference's tuner
-    (tilec/tune.py:82,148).
+    take any M, and K splits too when their own tiles cannot fill the CUs
+    (for tiles small enough to split, at least 4 K steps per split).  This
+    is the search space of tune.bench / tune.pick, as `mm_configs` is for
+    the reference's tuner (tilec/tune.py:82,148).
     """
     code = _dtype_code_name(dtype)
     out = []
@@ -100,7 +101,36 @@ def hip_configs(M, K, N, dtype="f32"):
                 out.append((v["name"], s))
         else:
             out.append((v["name"], 1))
+            tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
+            if tiles < SMALL_OUTPUT_TILES and tile_can_split(v):
+                seen = {1}
+                for s in _GEMM_SPLITS:
+                    eff = _gemm_splits(K, s, v["bk"])
+                    if eff in seen or cdiv(K, v["bk"]) < 4 * eff:
+                        continue
+                    seen.add(eff)
+                    out.append((v["name"], s))
     return out
+
+
+_GEMM_SPLITS = (2, 4, 8, 16)
+SPLIT_MAX_ACC_PER_THREAD = 64  # tilec_amd/csrc/common.h, kSplitMaxAccPerThread
+
+
+def tile_can_split(v):
+    """Whether a tile-GEMM variant splits K (its threads hold at most 64
+    accumulators; csrc/common.h, tile_can_split)."""
+    return v["bm"] * v["bn"] <= SPLIT_MAX_ACC_PER_THREAD * 64 * v["waves"]
+
+
+def _gemm_splits(K, split_k, bk):
+    """Splits a tile GEMM actually runs (csrc/common.h, gemm_split_geom)."""
+    total = cdiv(K, bk)
+    if total <= 0:
+        return 1
+    s = min(max(split_k, 1), total)
+    steps = cdiv(total, s)
+    return cdiv(total, steps)
 
 
 SMALL_OUTPUT_TILES = 256  # MI355X CUs: 64x64 output tiles below this leave CUs idle
