@@ -107,10 +107,12 @@ __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b
 // line).  The workgroup that brings the count to S resets the counter, adds
 // the S partials in split order (its own from registers), leaves the sums in
 // `v` and returns true; the others return false.  The order of additions
-// depends only on S, so results are deterministic.  Coherence across XCDs
-// without cache-wide fences: agent-coherent (sc1) data accesses, waits before
-// the barrier, a relaxed agent-scope atomic for the count.  The host keeps
-// S * tiles * NV * NT * 16 bytes below 2^31.
+// depends only on S, so results are deterministic.  Values whose `live` flag
+// is false (outside the output: never stored) are neither published nor read
+// back, so partial traffic scales with the valid part of a tile.  Coherence
+// across XCDs without cache-wide fences: agent-coherent (sc1) data accesses,
+// waits before the barrier, a relaxed agent-scope atomic for the count.  The
+// host keeps S * tiles * NV * NT * 16 bytes below 2^31.
 // ---------------------------------------------------------------------------
 constexpr int kSplitCounterStride = 64;  // uint32s between tile counters
 // Tile kernels split K only when a thread holds at most this many fp32
@@ -122,12 +124,14 @@ __host__ __device__ constexpr bool tile_can_split(int bm, int bn, int waves) {
 }
 
 template <int NT, int NV>
-__device__ __forceinline__ bool splitk_combine(f32x4 (&v)[NV], int split, int S, int tile, int tiles,
-                                               float* __restrict__ ws, unsigned* __restrict__ counters,
+__device__ __forceinline__ bool splitk_combine(f32x4 (&v)[NV], const bool (&live)[NV], int split, int S, int tile,
+                                               int tiles, float* __restrict__ ws, unsigned* __restrict__ counters,
                                                int* last_flag) {
   const uint32_t tid = threadIdx.x;
   const BufRsrc rw = make_rsrc(ws);
-  auto off = [&](int s, int q) { return 16u * ((uint32_t)((s * tiles + tile) * NV + q) * NT + tid); };
+  auto off = [&](int s, int q) {
+    return live[q] ? 16u * ((uint32_t)((s * tiles + tile) * NV + q) * NT + tid) : kOob;
+  };
 #pragma unroll
   for (int q = 0; q < NV; ++q) store_f32x4_coherent(rw, off(split, q), v[q]);
   __builtin_amdgcn_s_waitcnt(0);
@@ -176,10 +180,14 @@ __device__ __forceinline__ bool splitk_combine(f32x4 (&v)[NV], int split, int S,
 
 // splitk_combine for the TM x TN blocks of 32x32 MFMA accumulators of the
 // tile kernels: true (with the summed tile in acc) in the last split only.
+// Block (i, j) register r of this lane is output row row_base + 32 i +
+// 8 (r / 4) + r % 4, column col_base + 32 j (the 32x32 MFMA layout), so
+// float4 q of a block is 4 consecutive rows of one column: live when its
+// first row is below M and its column below N.
 template <int TM, int TN, int NT>
 __device__ __forceinline__ bool splitk_tile(f32x16 (&acc)[TM][TN], int split, int S, int tile, int tiles,
                                             float* __restrict__ ws, unsigned* __restrict__ counters,
-                                            int* last_flag) {
+                                            int* last_flag, int row_base, int col_base, int M, int N) {
   constexpr int NV = TM * TN * 4;
   if constexpr (TM * TN * 16 > kSplitMaxAccPerThread) {
     return true;  // never split (the host passes S == 1 for these tiles)
@@ -193,7 +201,15 @@ __device__ __forceinline__ bool splitk_tile(f32x16 (&acc)[TM][TN], int split, in
       for (int q = 0; q < 4; ++q)
         v[(i * TN + j) * 4 + q] =
             f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-  if (!splitk_combine<NT, NV>(v, split, S, tile, tiles, ws, counters, last_flag)) return false;
+  bool live[NV];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        live[(i * TN + j) * 4 + q] = (row_base + 32 * i + 8 * q < M) & (col_base + 32 * j < N);
+  if (!splitk_combine<NT, NV>(v, live, split, S, tile, tiles, ws, counters, last_flag)) return false;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll

@@ -320,13 +320,13 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
 
   // Split K: publish this workgroup's partial tile; the last of the tile's
   // splits adds them in split order and writes C.
-  if (S > 1 && !splitk_tile<P::TM, P::TN, P::NT>(acc, split, S, blockIdx.x, gridDim.x, ws, counters, &last_flag))
-    return;
-
   // Epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each block.
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
   const int row_base = m0 + wm * P::WTM + 4 * h;
   const int col_base = n0 + wn * P::WTN + (lane & 31);
+  if (S > 1 && !splitk_tile<P::TM, P::TN, P::NT>(acc, split, S, blockIdx.x, gridDim.x, ws, counters, &last_flag,
+                                                  row_base, col_base, M, N))
+    return;
 #pragma unroll
   for (int i = 0; i < P::TM; ++i)
 #pragma unroll

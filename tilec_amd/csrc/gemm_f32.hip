@@ -239,12 +239,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     __syncthreads();
   }
 
-  if (S > 1 && !splitk_tile<P::TM, P::TN, P::NT>(acc, split, S, blockIdx.x, gridDim.x, ws, counters, &last_flag))
-    return;
-
   // Epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each block.
   const int row_base = m0 + wm * P::WTM + 4 * khalf;
   const int col_base = n0 + bcol;
+  if (S > 1 && !splitk_tile<P::TM, P::TN, P::NT>(acc, split, S, blockIdx.x, gridDim.x, ws, counters, &last_flag,
+                                                  row_base, col_base, M, N))
+    return;
 #pragma unroll
   for (int i = 0; i < P::TM; ++i)
 #pragma unroll
