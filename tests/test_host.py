@@ -97,7 +97,7 @@ def test_hip_configs_rules():
                 assert eff == 1 or (ext.tile_can_split(v) and tiles < ext.SMALL_OUTPUT_TILES
                                     and ext.cdiv(K, v["bk"]) >= 4 * eff)
         has_skinny = any(names[n]["family"] == _lib.FAMILY_SKINNY for n, _ in cfgs)
-        assert has_skinny == (ext.skinny_regime(M, N) and dt == "f32")
+        assert has_skinny == ext.skinny_regime(M, N, dt)
     # Few tiles: the tile GEMMs that can split are offered split configs.
     assert ("gemm_bf16_128x128x64_r4", 8) in ext.hip_configs(1, 4096, 4096, "bf16")
     assert ("gemm_f32_128x64x16_w2x2", 4) in ext.hip_configs(1024, 1024, 1024, "f32")
@@ -305,5 +305,6 @@ def test_select_variant_rules():
     assert names[L.tilec_select_variant(1, 4096, 4096, 0)].startswith("skinny_f32")
     assert names[L.tilec_select_variant(4096, 4096, 4096, 0)].startswith("gemm_f32")
     assert names[L.tilec_select_variant(8192, 8192, 8192, 1)].startswith("gemm_bf16")
-    assert names[L.tilec_select_variant(4, 4096, 4096, 1)].startswith("gemm_bf16")
+    assert names[L.tilec_select_variant(4, 4096, 4096, 1)].startswith("skinny_bf16")
+    assert names[L.tilec_select_variant(17, 4096, 4096, 1)].startswith("gemm_bf16")
     assert L.tilec_select_variant(4, 4, 4, 5) == -_lib.ERR_TYPE

@@ -175,6 +175,28 @@ def test_skinny_shapes_and_splits():
             say(f"skinny m={m} k={k} n={n} ok")
 
 
+def test_skinny_bf16():
+    """bf16 inputs on the streaming kernel (widened to fp32 in registers):
+    aligned and unaligned shapes, every split the tuner may pick."""
+    for m in (1, 4, 16):
+        for k, n in [(64, 128), (1000, 136), (4096, 4096), (4097, 130), (333, 1000)]:
+            a16 = O.bf16_round(O.normal((m, k), 11 * m + k))
+            b16 = O.bf16_round(O.normal((k, n), 11 * m + k + 1))
+            ref = O.matmul_bf16_f64(a16, b16)
+            cfgs = [c for c in ext.hip_configs(m, k, n, "bf16") if c[0].startswith("skinny")]
+            assert cfgs
+            for cfg in cfgs:
+                got = run(dev_bf16(a16), dev_bf16(b16), cfg)
+                assert O.rel_l2(got, ref) <= 1e-5, (cfg, (m, k, n))
+            say(f"skinny bf16 m={m} k={k} n={n}: {len(cfgs)} configs ok")
+    rng = np.random.default_rng(3)
+    a = rng.integers(-3, 4, (9, 2000)).astype(np.float32)
+    b = rng.integers(-3, 4, (2000, 300)).astype(np.float32)
+    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    for cfg in [("skinny_bf16_w4_b1", 1), ("skinny_bf16_w8_b2", 8), ("skinny_bf16_w4_b2", 3)]:
+        np.testing.assert_array_equal(run(dev(a).to(torch.bfloat16), dev(b).to(torch.bfloat16), cfg), want)
+
+
 def test_skinny_row_blocks():
     """M > 16 on the streaming kernel: one grid row block per 16 rows of x1,
     each with its own partial slots and counters (every skinny config the

@@ -18,8 +18,8 @@ namespace tilec {
 const VariantDesc* skinny_variants(int* count);
 const VariantDesc* gemm_f32_variants(int* count);
 const VariantDesc* gemm_bf16_variants(int* count);
-size_t skinny_counter_bytes(int64_t M, int64_t N, int64_t K, int split_k);
-size_t skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, int split_k);
+size_t skinny_counter_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
+size_t skinny_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 int64_t skinny_effective_splits(int64_t N, int64_t K, int split_k);
 }  // namespace tilec
 
@@ -62,11 +62,11 @@ constexpr int kCUs = 256;                               // MI355X compute units
 
 // The skinny kernel addresses x2 within one 16-row block with 32-bit byte
 // offsets (row * ldx2 * 4, row < 16, must stay < 2^31), and its split-K
-// partials with 32-bit offsets (splits * row blocks * slabs * 4 KiB < 2^31).
-// Row blocks of 16 are its grid's z dimension (at most 65535).
+// partials with 32-bit offsets (splits * row blocks * slabs * 16 * slab
+// width * 4 bytes < 2^31).  Row blocks of 16 are its grid's z dimension
+// (at most 65535).
 constexpr int64_t kSkinnyMaxLdx1 = int64_t(1) << 25;
 constexpr int64_t kSkinnyMaxLdx2 = int64_t(1) << 25;
-constexpr int64_t kSkinnyMaxPartials = int64_t(1) << 19;  // splits * row blocks * slabs
 constexpr int64_t kSkinnyMaxRowBlocks = 65535;
 
 bool skinny_fits(int64_t ldx1, int64_t ldx2) { return ldx1 < kSkinnyMaxLdx1 && ldx2 < kSkinnyMaxLdx2; }
@@ -107,6 +107,9 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
     }
     return find("gemm_f32_64x64x16_w2x2");
   }
+  // bf16: the streaming kernel for M <= 16 (it runs fp32 MFMAs on widened
+  // inputs, so more rows are better served by the bf16 tile GEMMs).
+  if (M <= 16 && skinny_fits(ldx1, ldx2)) return find("skinny_bf16_w8_b1");
   static const char* order[] = {"gemm_bf16_256x256x64_r2", "gemm_bf16_256x128x64_r3", "gemm_bf16_128x128x64_r4"};
   for (const char* nm : order) {
     const int v = find(nm);
@@ -185,7 +188,7 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
                   (long long)(kSkinnyMaxRowBlocks * d->bm), (long long)M);
     if (splits > 65535)
       return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
-    if (splits > 1 && splits * cells >= kSkinnyMaxPartials)
+    if (splits > 1 && splits * cells * d->bm * d->bn * 4 >= (int64_t(1) << 31))
       return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits x %lld output blocks of partials is too many",
                   d->name, (long long)splits, (long long)cells);
   }
@@ -215,11 +218,11 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
     if (ldx2 < N) return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < N=%lld", (long long)ldx2, (long long)N);
   }
   const bool skinny = d->family == TILEC_FAMILY_SKINNY;
-  const size_t need = skinny ? skinny_workspace_bytes(M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
+  const size_t need = skinny ? skinny_workspace_bytes(dtype, M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu workspace bytes (got %zu)", d->name, need,
                 workspace == nullptr ? (size_t)0 : workspace_bytes);
-  const size_t need_cnt = skinny ? skinny_counter_bytes(M, N, K, s) : gemm_counter_bytes(d, M, N, K, s);
+  const size_t need_cnt = skinny ? skinny_counter_bytes(dtype, M, N, K, s) : gemm_counter_bytes(d, M, N, K, s);
   if (need_cnt > 0 && (counters == nullptr || counter_bytes < need_cnt))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu bytes of counters (got %zu)", d->name, need_cnt,
                 counters == nullptr ? (size_t)0 : counter_bytes);
@@ -251,7 +254,7 @@ size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t dty
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
   if (M == 0 || N == 0) return 0;
-  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(dtype, M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
 }
 
 size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
@@ -260,7 +263,7 @@ size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
   if (M == 0 || N == 0) return 0;
-  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(M, N, K, s) : gemm_counter_bytes(d, M, N, K, s);
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(dtype, M, N, K, s) : gemm_counter_bytes(d, M, N, K, s);
 }
 
 int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {

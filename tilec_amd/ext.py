@@ -74,8 +74,8 @@ _SKINNY_SPLITS = (1, 2, 4, 8, 16, 32, 64)
 def hip_configs(M, K, N, dtype="f32"):
     """Every (variant, split_k) the library can run for out[M,N] = x1[M,K]·x2[K,N].
 
-    The skinny family (a K split, 16-row blocks) is offered for M <= 16 and
-    for outputs too small to fill the chip with 64x64 tiles; the tile GEMMs
+    The skinny family (a K split, 16-row blocks) is offered for M <= 16 and,
+    for fp32, outputs too small to fill the chip with 64x64 tiles; the tile GEMMs
     take any M, and K splits too when their own tiles cannot fill the CUs
     (for tiles small enough to split, at least 4 K steps per split).  This
     is the search space of tune.bench / tune.pick, as `mm_configs` is for
@@ -86,7 +86,7 @@ def hip_configs(M, K, N, dtype="f32"):
     for v in _lib.variants():
         if v["dtype"] != code or (v["max_m"] and M > v["max_m"]):
             continue
-        if v["family"] == _lib.FAMILY_SKINNY and not skinny_regime(M, N):
+        if v["family"] == _lib.FAMILY_SKINNY and not skinny_regime(M, N, code):
             continue
         if v["family"] == _lib.FAMILY_SKINNY:
             # A workgroup takes at most BK (the variant's K-slice cap) rows
@@ -136,10 +136,14 @@ def _gemm_splits(K, split_k, bk):
 SMALL_OUTPUT_TILES = 256  # MI355X CUs: 64x64 output tiles below this leave CUs idle
 
 
-def skinny_regime(M, N):
-    """Whether the streaming (skinny) kernels are candidates: M <= 16, or
-    fewer 64x64 output tiles than CUs (the rule of tilec_select_variant)."""
-    return M <= 16 or cdiv(M, 64) * cdiv(N, 64) < SMALL_OUTPUT_TILES
+def skinny_regime(M, N, dtype="f32"):
+    """Whether the streaming (skinny) kernels are candidates: M <= 16, or for
+    fp32 also fewer 64x64 output tiles than CUs (the rule of
+    tilec_select_variant).  bf16 inputs stream through fp32 MFMAs, so past
+    16 rows the bf16 tile GEMMs (with a K split) serve them better."""
+    if M <= 16:
+        return True
+    return _dtype_code_name(dtype) == _lib.F32 and cdiv(M, 64) * cdiv(N, 64) < SMALL_OUTPUT_TILES
 
 
 def _skinny_splits(K, split_k, kc_max):

@@ -80,7 +80,7 @@ def operands_for(M, K, N, x2):
     from HBM would not; otherwise x2 alone."""
     from . import ext
     nbytes = x2.numel() * x2.element_size()
-    if not ext.skinny_regime(M, N) or nbytes < (1 << 20):
+    if not ext.skinny_regime(M, N, x2.dtype) or nbytes < (1 << 20):
         return [x2]
     copies = min(16, max(1, -(-ROTATE_BYTES // nbytes)))
     return [x2] + [x2.clone() for _ in range(copies - 1)]
