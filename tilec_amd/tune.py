@@ -148,6 +148,7 @@ CONFIG_SHAPES = [
     (1024, 1024, 1024, "f32"), (2048, 2048, 2048, "f32"), (4096, 4096, 4096, "f32"),
     (127, 1000, 513, "f32"), (513, 3001, 127, "f32"), (1000, 4097, 3001, "f32"), (3001, 513, 1000, "f32"),
     (8192, 8192, 8192, "bf16"), (4096, 4096, 4096, "bf16"),
+    (1, 4096, 4096, "bf16"), (16, 4096, 4096, "bf16"),
 ]
 
 
@@ -157,7 +158,7 @@ def shapes(n=500, seed=0):
     Keeps the reference's log-uniform generator with its size limits
     (tilec/tune.py:54-65; there x1 is [M1,N] and x2 is [N,M2], so its N is
     our K) and adds the regimes MI355X serves differently: skinny M in
-    [1, 16], bf16, and ragged sizes.
+    [1, 16] (fp32 and bf16), bf16 tile GEMMs, and ragged sizes.
     """
     rng = random.Random(seed)
     out = set(CONFIG_SHAPES)
@@ -169,9 +170,11 @@ def shapes(n=500, seed=0):
         dtype = "f32"
         if rng.random() < 0.5:
             K = 1 << round(math.log2(K))
-        if kind < 0.3:                      # skinny
+        if kind < 0.3:                      # skinny (a third of them bf16)
             M = rng.randint(1, 16)
             N = round(2 ** rng.uniform(8, 14))
+            if kind < 0.1:
+                dtype = "bf16"
         elif kind < 0.55:                   # bf16 tile GEMM
             dtype = "bf16"
         if M * K * N <= 1 << 33 and M * K <= 1 << 26 and K * N <= 1 << 26:
