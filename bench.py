@@ -96,38 +96,45 @@ def bench_square(args):
 
 
 def bench_skinny(steps=200):
-    """M in {1,4,16}: HBM GB/s from graph-replayed launches over rotating x2."""
+    """M in {1,4,16} fp32 and {1,16} bf16 at K=N=4096: HBM GB/s from graph-replayed
+    launches over rotating x2 copies (>= 512 MB per dtype, so neither L2 nor the
+    256 MB MALL serves a repeat)."""
     import torch
     from oracle import oracle as O
     from tilec_amd import ext
     K = N = 4096
-    nbuf = 8
-    x2s = [torch.from_numpy(O.normal((K, N), 3 + 1000 * i)).cuda() for i in range(nbuf)]
     out = {}
-    for M in (1, 4, 16):
-        x1 = torch.from_numpy(O.normal((M, K), 2)).cuda()
-        cfg = kernel_name_for(M, K, N, "f32")
-        for i in range(nbuf):  # warm up: workspace exists before capture
-            ext.matrix_mul(x1, x2s[i])
-        torch.cuda.synchronize()
-        reps = 4 * nbuf
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            ext.matrix_mul(x1, x2s[0])
+    for dtype, Ms in (("f32", (1, 4, 16)), ("bf16", (1, 16))):
+        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+        esz = 4 if dtype == "f32" else 2
+        nbuf = (512 << 20) // (esz * K * N)
+        x2s = [torch.from_numpy(O.normal((K, N), 3 + 1000 * i)).to(tdt).cuda() for i in range(nbuf)]
+        for M in Ms:
+            x1 = torch.from_numpy(O.normal((M, K), 2)).to(tdt).cuda()
+            cfg = kernel_name_for(M, K, N, dtype)
+            for i in range(nbuf):  # warm up: workspace exists before capture
+                ext.matrix_mul(x1, x2s[i])
             torch.cuda.synchronize()
-            with torch.cuda.graph(g, stream=s):
-                outs = [ext.matrix_mul(x1, x2s[i % nbuf]) for i in range(reps)]
-        torch.cuda.synchronize()
-        replays = max(1, steps // reps)
-        with torch.cuda.stream(s):
-            ms = timed(g.replay, replays, 2, stream=s) / reps
-        del outs
-        nbytes = 4 * (M * K + K * N + M * N)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out[f"M{M}"] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, config=list(cfg))
-        log(f"skinny M={M}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({cfg})")
+            reps = 4 * nbuf
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                ext.matrix_mul(x1, x2s[0])
+                torch.cuda.synchronize()
+                with torch.cuda.graph(g, stream=s):
+                    outs = [ext.matrix_mul(x1, x2s[i % nbuf]) for i in range(reps)]
+            torch.cuda.synchronize()
+            replays = max(1, steps // reps)
+            with torch.cuda.stream(s):
+                ms = timed(g.replay, replays, 2, stream=s) / reps
+            del outs
+            nbytes = esz * (M * K + K * N) + 4 * M * N
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            key = f"M{M}" if dtype == "f32" else f"bf16_M{M}"
+            out[key] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, config=list(cfg))
+            log(f"skinny {dtype} M={M}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({cfg})")
+        del x2s
     return out
 
 

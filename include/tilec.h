@@ -12,9 +12,14 @@
  * `matrix_mul(x1, x2)` (tilec/ext.py:66-67).
  *
  * Conventions shared by all entry points
- *   - Matrices are row-major with unit column stride; ld* is the row stride in
- *     elements (>= the row length).  After the reference's `.contiguous()`
- *     (tilec/ext.py:59-60) ld == the number of columns.
+ *   - The output is row-major with unit column stride; ldo is its row stride
+ *     in elements (>= N).  Each input is row-major (ld* = row stride >= its
+ *     number of columns) or, when its `layout` bit is set, column-major
+ *     (ld* = column stride >= its number of rows) — the transposed view
+ *     x.T of a contiguous matrix, read in place.  The reference makes every
+ *     input row-major contiguous first (`.contiguous()`, tilec/ext.py:59-60;
+ *     then ld == the number of columns); strided and transposed views skip
+ *     that copy here.
  *   - Outputs are float32.  Inputs are float32, or bfloat16 (fp32 accumulate).
  *   - Nothing here allocates device memory, synchronizes, or reads the device
  *     back: work is enqueued on `stream` (a hipStream_t; NULL = the legacy
@@ -53,6 +58,10 @@ extern "C" {
                               /* M <= 16, or outputs of few 64x64 tiles         */
 #define TILEC_FAMILY_GEMM 1   /* LDS-staged MFMA tile GEMM                      */
 
+/* Operand layouts: bits of tilec_matmul's `layout` (0 = both row-major). */
+#define TILEC_X1_COL_MAJOR 1 /* x1 element (m, k) at x1[m + k * ldx1], ldx1 >= M */
+#define TILEC_X2_COL_MAJOR 2 /* x2 element (k, n) at x2[k + n * ldx2], ldx2 >= K */
+
 /* Pass as `variant` to let the library pick with its built-in rule. */
 #define TILEC_VARIANT_AUTO (-1)
 
@@ -66,6 +75,10 @@ extern "C" {
  * tile sizes select a compiled specialization (tilec/jit.py:66-76);
  * `split_k` (0 = automatic) splits the reduction dimension across
  * workgroups, the role of the legacy `split` config (tilec/ext.py:37,48-51).
+ *
+ * `layout` (TILEC_X1_COL_MAJOR | TILEC_X2_COL_MAJOR) says how x1 and x2 are
+ * stored; every variant takes every layout.  The reference has no such
+ * argument: it copies each input to row-major first (tilec/ext.py:59-60).
  *
  * M == 0 or N == 0 enqueues nothing.  K == 0 writes zeros (the reference's
  * accumulator starts at zero and its K loop runs no iterations).
@@ -82,16 +95,16 @@ extern "C" {
  */
 int tilec_matmul(const void* x1, const void* x2, float* out,
                  int64_t M, int64_t N, int64_t K,
-                 int64_t ldx1, int64_t ldx2, int64_t ldo,
+                 int64_t ldx1, int64_t ldx2, int64_t ldo, int32_t layout,
                  int32_t dtype, int32_t variant, int32_t split_k,
                  void* workspace, size_t workspace_bytes,
                  void* counters, size_t counter_bytes, void* stream);
 
 /*
  * Bytes of scratch (`workspace`) tilec_matmul needs for these arguments
- * (0 if none).  Replaces nothing in the reference (its kernel needs no
- * scratch); the caller allocates it the way `_matrix_mul_tiled` allocates
- * `out` (tilec/ext.py:61).
+ * (0 if none; the same for every layout).  Replaces nothing in the
+ * reference (its kernel needs no scratch); the caller allocates it the way
+ * `_matrix_mul_tiled` allocates `out` (tilec/ext.py:61).
  */
 size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K,
                                     int32_t dtype, int32_t variant,

@@ -211,7 +211,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_variants():
     L = _lib.lib()
-    assert L.tilec_version() == 10000
+    assert L.tilec_version() == 10100
     vs = _lib.variants()
     assert len(vs) == L.tilec_num_variants() > 0
     assert len({v["name"] for v in vs}) == len(vs)
@@ -222,12 +222,13 @@ def test_version_and_variants():
 
 
 def _call(M=8, N=8, K=8, ldx1=None, ldx2=None, ldo=None, dtype=0, variant=-1, split=0,
-          ws=None, ws_bytes=0, cnt=None, cnt_bytes=0, x1=16, x2=16, out=16):
+          ws=None, ws_bytes=0, cnt=None, cnt_bytes=0, x1=16, x2=16, out=16, layout=0):
     # Non-null dummy pointers: every case below must fail validation before launch.
     L = _lib.lib()
-    return L.tilec_matmul(x1, x2, out, M, N, K, ldx1 if ldx1 is not None else K,
-                          ldx2 if ldx2 is not None else N, ldo if ldo is not None else N,
-                          dtype, variant, split, ws, ws_bytes, cnt, cnt_bytes, None)
+    c1, c2 = layout & _lib.X1_COL_MAJOR, layout & _lib.X2_COL_MAJOR
+    return L.tilec_matmul(x1, x2, out, M, N, K, ldx1 if ldx1 is not None else (M if c1 else K),
+                          ldx2 if ldx2 is not None else (K if c2 else N), ldo if ldo is not None else N,
+                          layout, dtype, variant, split, ws, ws_bytes, cnt, cnt_bytes, None)
 
 
 def test_abi_rejects_bad_arguments_before_launch():
@@ -238,6 +239,13 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert _call(ldx1=3) == _lib.ERR_VALUE
     assert _call(ldx2=3) == _lib.ERR_VALUE
     assert _call(ldo=3) == _lib.ERR_VALUE
+    # Column-major operands: the stride runs over columns and covers the rows.
+    assert _call(M=8, K=4, ldx1=4, layout=_lib.X1_COL_MAJOR) == _lib.ERR_VALUE
+    assert "ldx1=4 < M=8" in _lib.last_error()
+    assert _call(K=8, N=4, ldx2=4, layout=_lib.X2_COL_MAJOR) == _lib.ERR_VALUE
+    assert "ldx2=4 < K=8" in _lib.last_error()
+    assert _call(layout=4) == _lib.ERR_VALUE
+    assert "layout" in _lib.last_error()
     assert _call(out=None) == _lib.ERR_VALUE
     assert _call(x1=None) == _lib.ERR_VALUE
     assert _call(variant=10 ** 6) == _lib.ERR_UNSUPPORTED
@@ -247,6 +255,11 @@ def test_abi_rejects_bad_arguments_before_launch():
     # The streaming kernel takes any M in 16-row blocks, up to 65535 of them.
     assert _call(M=16 * 65535 + 1, variant=skinny) == _lib.ERR_UNSUPPORTED
     assert "M <=" in _lib.last_error()
+    # Its 32-bit block offsets bound the strides: column-major x2 spans a
+    # slab of 64 columns, so its column stride stays below 2^23.
+    assert _call(M=4, N=64, K=64, ldx2=1 << 23, variant=skinny, layout=_lib.X2_COL_MAJOR) == _lib.ERR_UNSUPPORTED
+    assert "2^23" in _lib.last_error()
+    assert _call(M=4, N=64, K=64, ldx2=1 << 25, variant=skinny) == _lib.ERR_UNSUPPORTED
     assert _call(variant=bf16, dtype=0) == _lib.ERR_UNSUPPORTED
     # Tile GEMMs split K (workspace required) unless a thread's tile is too big to.
     assert _call(M=64, N=64, K=4096, variant=gemm, split=2) == _lib.ERR_WORKSPACE
@@ -308,3 +321,38 @@ def test_select_variant_rules():
     assert names[L.tilec_select_variant(4, 4096, 4096, 1)].startswith("skinny_bf16")
     assert names[L.tilec_select_variant(17, 4096, 4096, 1)].startswith("gemm_bf16")
     assert L.tilec_select_variant(4, 4, 4, 5) == -_lib.ERR_TYPE
+
+
+def test_operand_layouts_read_in_place():
+    """Row-strided and transposed views go to the kernels as they are (layout
+    bits and leading dimensions), everything else is copied to row-major."""
+    a = torch.zeros(6, 10)
+    t, ld, col = ext._operand(a, 6, 10)
+    assert (t.data_ptr(), ld, col) == (a.data_ptr(), 10, False)
+    v = a[:, 2:7]                                   # row stride 10 >= 5 columns
+    t, ld, col = ext._operand(v, 6, 5)
+    assert (t.data_ptr(), ld, col) == (v.data_ptr(), 10, False)
+    at = a.t()                                      # [10, 6] column-major, column stride 10
+    t, ld, col = ext._operand(at, 10, 6)
+    assert (t.data_ptr(), ld, col) == (a.data_ptr(), 10, True)
+    sub = a[1:5, :].t()                             # [10, 4] column-major, column stride 10 >= 10 rows
+    t, ld, col = ext._operand(sub, 10, 4)
+    assert (t.data_ptr(), ld, col) == (sub.data_ptr(), 10, True)
+    # vectors: size-1 dimensions impose no stride, row-major preferred
+    row = a[2:3, :]
+    assert ext._operand(row, 1, 10)[1:] == (10, False)
+    colv = a[:, 3:4]
+    assert ext._operand(colv, 6, 1)[1:] == (10, False)
+    colt = a[3:4, :].t()                            # [10, 1]: stride (1, 10)
+    assert ext._operand(colt, 10, 1)[1:] == (1, False)  # element (r, 0) at r * 1
+    # neither layout: every other element, broadcast -> contiguous copies
+    every_other = a.t()[:, ::2]                     # [10, 3], strides (1, 20): column-major, ld 20
+    t, ld, col = ext._operand(every_other, 10, 3)
+    assert (t.data_ptr(), ld, col) == (a.data_ptr(), 20, True)
+    for x, (r, c) in ((a[:, ::2], (6, 5)), (torch.zeros(1, 10).expand(6, 10), (6, 10)), (a[::2, ::2], (3, 5))):
+        t, ld, col = ext._operand(x, r, c)
+        assert t.is_contiguous() and ld == c and col is False
+        assert torch.equal(t, x)
+    assert ext.layout_of(a, a.t()) == _lib.X2_COL_MAJOR
+    assert ext.layout_of(a.t(), a) == _lib.X1_COL_MAJOR
+    assert ext.layout_of(a.t(), a.t().t()) == _lib.X1_COL_MAJOR

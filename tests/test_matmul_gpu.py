@@ -348,7 +348,7 @@ def test_strided_and_transposed_inputs():
     a, b = O.normal((300, 200), 13), O.normal((200, 150), 14)
     ref = O.matmul_f64(a, b)
     da, db = dev(a), dev(b)
-    # row-strided views (no copy) and transposed views (.contiguous copy)
+    # row-strided and transposed views are read in place
     big_a = torch.zeros(300, 260, device="cuda")
     big_a[:, :200] = da
     big_b = torch.zeros(200, 170, device="cuda")
@@ -359,7 +359,127 @@ def test_strided_and_transposed_inputs():
     # skinny path with a strided x2
     a1 = O.normal((4, 200), 15)
     assert O.rel_l2(run(dev(a1), big_b[:, :150]), O.matmul_f64(a1, b)) <= O.TOL_F32
+    # a view that is neither row- nor column-major ([300, 100], strides (260, 2)) is copied first
+    b2 = O.normal((100, 150), 16)
+    assert O.rel_l2(run(big_a[:, :200][:, ::2], dev(b2)), O.matmul_f64(np.ascontiguousarray(a[:, ::2]), b2)) <= O.TOL_F32
     say("strided ok")
+
+
+# ---------------------------------------------------------------------------
+# Column-major operands (transposed views), read in place by every variant
+# ---------------------------------------------------------------------------
+
+LAYOUTS = [_lib.X1_COL_MAJOR, _lib.X2_COL_MAJOR, _lib.X1_COL_MAJOR | _lib.X2_COL_MAJOR]
+
+
+def laid_out(x, col, pad=0):
+    """The [r, c] device matrix x as a column-major view (x.T of a [c, r + pad]
+    row-major buffer, leading dimension r + pad) when col, else as is."""
+    if not col:
+        return x
+    r, c = x.shape
+    buf = torch.zeros((c, r + pad), dtype=x.dtype, device=x.device)
+    buf[:, :r] = x.t()
+    return buf[:, :r].t()
+
+
+def run_layout(x1, x2, layout, config=None, pad=0):
+    v1 = laid_out(x1, layout & _lib.X1_COL_MAJOR, pad)
+    v2 = laid_out(x2, layout & _lib.X2_COL_MAJOR, pad)
+    # a vector is both row- and column-major (ext takes row-major): check
+    # the layout bits of the operands that are matrices
+    got = ext.layout_of(v1, v2)
+    for bit, x in ((_lib.X1_COL_MAJOR, x1), (_lib.X2_COL_MAJOR, x2)):
+        if min(x.shape) > 1:
+            assert got & bit == layout & bit, (layout, got, tuple(x.shape))
+    return run(v1, v2, config)
+
+
+LAYOUT_SHAPES = RAGGED + [(64, 256, 256), (200, 516, 132), (256, 512, 256), (264, 200, 392), (8, 1032, 520)]
+
+
+@pytest.mark.parametrize("name", f32_variants())
+def test_f32_variant_layouts(name):
+    v = _lib.variants()[_lib.variant_id(name)]
+    for layout in LAYOUTS:
+        for i, (m, k, n) in enumerate(LAYOUT_SHAPES):
+            a, b = O.normal((m, k), 500 + 2 * i), O.normal((k, n), 501 + 2 * i)
+            ref = O.matmul_f64(a, b)
+            splits = [1] if v["family"] == _lib.FAMILY_GEMM else [1, 3, 8]
+            for s in splits:
+                say(f"{name} layout {layout} split {s} shape {(m, k, n)}")
+                got = run_layout(dev(a), dev(b), layout, (name, s))
+                assert O.rel_l2(got, ref) <= O.TOL_F32, (name, layout, s, (m, k, n))
+
+
+@pytest.mark.parametrize("name", bf16_variants())
+def test_bf16_variant_layouts(name):
+    v = _lib.variants()[_lib.variant_id(name)]
+    for layout in LAYOUTS:
+        for i, (m, k, n) in enumerate(LAYOUT_SHAPES):
+            a16 = O.bf16_round(O.normal((m, k), 600 + 2 * i))
+            b16 = O.bf16_round(O.normal((k, n), 601 + 2 * i))
+            ref = O.matmul_bf16_f64(a16, b16)
+            splits = [1] if v["family"] == _lib.FAMILY_GEMM else [1, 3, 8]
+            for s in splits:
+                say(f"{name} layout {layout} split {s} shape {(m, k, n)}")
+                got = run_layout(dev_bf16(a16), dev_bf16(b16), layout, (name, s))
+                assert O.rel_l2(got, ref) <= 1e-5, (name, layout, s, (m, k, n))
+
+
+def test_layouts_padded_strides_and_splits():
+    """Column strides above the row count, and K splits of the tile GEMMs,
+    in every layout."""
+    cases = [((33, 1000, 65), "f32"), ((520, 2048, 300), "f32"), ((16, 4096, 512), "f32"),
+             ((520, 2048, 304), "bf16"), ((16, 4096, 512), "bf16")]
+    for (m, k, n), dt in cases:
+        a, b = O.normal((m, k), 700), O.normal((k, n), 701)
+        if dt == "bf16":
+            a, b = O.bf16_round(a), O.bf16_round(b)
+            x1, x2, ref, tol = dev_bf16(a), dev_bf16(b), O.matmul_bf16_f64(a, b), 1e-5
+        else:
+            x1, x2, ref, tol = dev(a), dev(b), O.matmul_f64(a, b), O.TOL_F32
+        for layout in LAYOUTS:
+            for cfg in ext.hip_configs(m, k, n, dt):
+                for pad in (0, 8, 3):
+                    say(f"padded {(m, k, n)} {dt} layout {layout} pad {pad} {cfg}")
+                    got = run_layout(x1, x2, layout, cfg, pad)
+                    assert O.rel_l2(got, ref) <= tol, ((m, k, n), dt, layout, pad, cfg)
+
+
+def test_golden_integer_products_layouts():
+    """Exact small-integer products are exact in every layout and variant."""
+    g = np.load(GOLDEN)
+    for i, (m, k, n) in enumerate(g["shapes"]):
+        m, k, n = int(m), int(k), int(n)
+        a = g[f"x1_{i}"].astype(np.float32)
+        b = g[f"x2_{i}"].astype(np.float32)
+        want = g[f"out_{i}"].astype(np.float32)
+        a16, b16 = O.bf16_round(a), O.bf16_round(b)
+        for layout in LAYOUTS:
+            for cfg in ext.hip_configs(m, k, n, "f32"):
+                say(f"golden {i} {(m, k, n)} f32 layout {layout} {cfg}")
+                np.testing.assert_array_equal(run_layout(dev(a), dev(b), layout, cfg), want)
+            for cfg in ext.hip_configs(m, k, n, "bf16"):
+                say(f"golden {i} {(m, k, n)} bf16 layout {layout} {cfg}")
+                np.testing.assert_array_equal(run_layout(dev_bf16(a16), dev_bf16(b16), layout, cfg), want)
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_gemv_weight_transposed(m):
+    """x @ W.T with W [N, K] row-major (a linear layer's weight), at the
+    config-1 size, with the tuned pick: the weight is read in place."""
+    k = n = 4096
+    x, w = O.normal((m, k), 800 + m), O.normal((n, k), 801 + m)
+    ref = O.matmul_f64(x, np.ascontiguousarray(w.T))
+    dx, dw = dev(x), dev(w)
+    assert ext.layout_of(dx, dw.t()) == _lib.X2_COL_MAJOR
+    got = run(dx, dw.t())
+    assert O.rel_l2(got, ref) <= O.TOL_F32
+    x16, w16 = O.bf16_round(x), O.bf16_round(w)
+    got16 = run(dev_bf16(x16), dev_bf16(w16).t())
+    assert O.rel_l2(got16, O.matmul_bf16_f64(x16, np.ascontiguousarray(w16.T))) <= 1e-5
+    say(f"gemv x @ W.T m={m} ok")
 
 
 def test_non_default_stream_and_ordering():

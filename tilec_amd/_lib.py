@@ -18,12 +18,13 @@ LIB_PATH = os.path.join(HERE, "libtilec_hip.so")
 OK, ERR_VALUE, ERR_TYPE, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_HIP = 0, 1, 2, 3, 4, 5
 F32, BF16 = 0, 1
 FAMILY_SKINNY, FAMILY_GEMM = 0, 1
+X1_COL_MAJOR, X2_COL_MAJOR = 1, 2  # layout bits
 VARIANT_AUTO = -1
 
 # Every function include/tilec.h declares: name -> (restype, argtypes).
 _i64, _i32, _vp, _sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t
 SIGNATURES = {
-    "tilec_matmul": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+    "tilec_matmul": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
                                     _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp]),
     "tilec_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
     "tilec_matmul_counter_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),

@@ -23,6 +23,7 @@ struct MatmulArgs {
   float* out;
   int64_t M, N, K;
   int64_t ldx1, ldx2, ldo;
+  int layout;            // TILEC_X1_COL_MAJOR | TILEC_X2_COL_MAJOR bits
   int split_k;           // resolved (>= 1)
   void* workspace;       // split-K partial sums (scratch)
   size_t workspace_bytes;

@@ -1,5 +1,6 @@
 // LDS-staged bf16 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x16_bf16):
-//   C[M,N] (fp32) = A[M,K] (bf16) · B[K,N] (bf16), fp32 accumulate.
+//   C[M,N] (fp32) = A[M,K] (bf16) · B[K,N] (bf16), fp32 accumulate; A and B
+//   each row- or column-major, read in place.
 //
 // Same tile semantics as the reference tile kernel `_matmul_tiled`
 // (tilec/ext.py:13-24) — zero accumulator, masked K steps with `other=0.0`,
@@ -27,10 +28,7 @@ struct GemmBf16 {
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
   static constexpr int LDS_K = BK + 8;  // row length in elements (16-byte pad)
-  static constexpr int A_Q = BM * BK / 8 / NT;  // 16-byte loads of A per thread
-  static constexpr int B_Q = BK * BN / 8 / NT;  // 16-byte loads of B per thread
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-  static_assert(BM * BK % (8 * NT) == 0 && BK * BN % (8 * NT) == 0, "tile loads must divide evenly");
   static_assert(BK % 16 == 0, "BK");
   static constexpr size_t kLds = sizeof(u16) * 2 * LDS_K * (BM + BN);
 };
@@ -52,12 +50,76 @@ __device__ __forceinline__ u16x8 ld8(const u16* __restrict__ p, bool ok_all, int
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool VEC>
+// One operand's tile per K step: R rows of its outer dimension (M for x1, N
+// for x2) by BK of K, global -> registers -> LDS.  KC: element (r, k) at
+// X[r * ld + k] (row-major x1, column-major x2), moved as 8 consecutive k;
+// otherwise at X[k * ld + r], moved as 8 consecutive r.  In LDS the tile is
+// S[r][k] with rows of BK + 8 elements: a KC group is one 16-byte store, the
+// other kind is transposed by 8 element stores.
+template <int R, int BK, int NT, bool KC, bool VEC>
+struct OperandBf16 {
+  static constexpr int Q = R * BK / 8 / NT;
+  static constexpr int LDS_K = BK + 8;
+  static_assert(R * BK % (8 * NT) == 0, "tile loads must divide evenly");
+  typedef u16x8 Regs[Q];
+
+  // Tile row and tile k of the first element of thread tid's group p.
+  __device__ __forceinline__ static void coord(int tid, int p, int& r, int& k) {
+    const int e = tid + p * NT;
+    if constexpr (KC) {
+      r = e / (BK / 8);
+      k = 8 * (e % (BK / 8));
+    } else {
+      k = e / (R / 8);
+      r = 8 * (e % (R / 8));
+    }
+  }
+
+  // K step kt of the tile at outer row r0 (of Rtot).  MASK: clamp + select
+  // at every edge; otherwise whole 16-byte groups.
+  __device__ __forceinline__ static void load(Regs& v, const u16* __restrict__ X, int64_t ld, int r0, int Rtot, int K,
+                                              int tid, int kt, bool mask) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int p = 0; p < Q; ++p) {
+      int tr, tk;
+      coord(tid, p, tr, tk);
+      const int gr = r0 + tr, gk = k0 + tk;
+      const int64_t at = KC ? (int64_t)gr * ld + gk : (int64_t)gk * ld + gr;
+      if (!mask) {
+        v[p] = ld8<VEC>(X + at, true, 8);
+      } else {
+        const int valid = KC ? (gr < Rtot ? max(0, min(8, K - gk)) : 0) : (gk < K ? max(0, min(8, Rtot - gr)) : 0);
+        v[p] = ld8<VEC>(X + (valid > 0 ? at : 0), valid == 8, valid);
+      }
+    }
+  }
+
+  __device__ __forceinline__ static void store(const Regs& v, u16* __restrict__ S, int tid) {
+#pragma unroll
+    for (int p = 0; p < Q; ++p) {
+      int tr, tk;
+      coord(tid, p, tr, tk);
+      if constexpr (KC) {
+        *reinterpret_cast<u16x8*>(S + tr * LDS_K + tk) = v[p];
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) S[(tr + c) * LDS_K + tk] = v[p][c];
+      }
+    }
+  }
+};
+
+// CA: x1 column-major (element (m, k) at A[m + k * lda]); CB: x2 column-major
+// (element (k, n) at B[k + n * ldb]).
+template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool CA, bool CB>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
     const u16* __restrict__ A, const u16* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
     unsigned* __restrict__ counters) {
   using P = GemmBf16<BM, BN, BK, WM, WN>;
+  using OpA = OperandBf16<BM, BK, P::NT, !CA, VEC>;
+  using OpB = OperandBf16<BN, BK, P::NT, CB, VEC>;
   extern __shared__ __align__(16) u16 lds_u16[];
   __shared__ int last_flag;
   u16* As = lds_u16;                          // [2][BM][LDS_K]
@@ -77,54 +139,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
   const int kt1 = min((K + BK - 1) / BK, kt0 + split_steps);
   const int nk_full = K / BK;
 
-  u16x8 ra[P::A_Q], rb[P::B_Q];
-
+  typename OpA::Regs ra;
+  typename OpB::Regs rb;
   auto gload = [&](int kt, bool mask) {
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int p = 0; p < P::A_Q; ++p) {
-      const int e = tid + p * P::NT;
-      const int i = e / (BK / 8), kq = e % (BK / 8);
-      const int gm = m0 + i, gk = k0 + 8 * kq;
-      if (!mask) {
-        ra[p] = ld8<VEC>(A + (int64_t)gm * lda + gk, true, 8);
-      } else {
-        const int valid = gm < M ? max(0, min(8, K - gk)) : 0;
-        const int64_t off = valid > 0 ? (int64_t)gm * lda + gk : 0;
-        ra[p] = ld8<VEC>(A + off, valid == 8, valid);
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < P::B_Q; ++p) {
-      const int e = tid + p * P::NT;
-      const int k = e / (BN / 8), jq = e % (BN / 8);
-      const int gk = k0 + k, gn = n0 + 8 * jq;
-      if (!mask) {
-        rb[p] = ld8<VEC>(B + (int64_t)gk * ldb + gn, true, 8);
-      } else {
-        const int valid = gk < K ? max(0, min(8, N - gn)) : 0;
-        const int64_t off = valid > 0 ? (int64_t)gk * ldb + gn : 0;
-        rb[p] = ld8<VEC>(B + off, valid == 8, valid);
-      }
-    }
+    OpA::load(ra, A, lda, m0, M, K, tid, kt, mask);
+    OpB::load(rb, B, ldb, n0, N, K, tid, kt, mask);
   };
-
   auto sstore = [&](int buf) {
-    u16* as = As + buf * BM * P::LDS_K;
-    u16* bs = Bs + buf * BN * P::LDS_K;
-#pragma unroll
-    for (int p = 0; p < P::A_Q; ++p) {
-      const int e = tid + p * P::NT;
-      const int i = e / (BK / 8), kq = e % (BK / 8);
-      *reinterpret_cast<u16x8*>(as + i * P::LDS_K + 8 * kq) = ra[p];
-    }
-#pragma unroll
-    for (int p = 0; p < P::B_Q; ++p) {
-      const int e = tid + p * P::NT;
-      const int k = e / (BN / 8), jq = e % (BN / 8);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) bs[(8 * jq + c) * P::LDS_K + k] = rb[p][c];
-    }
+    OpA::store(ra, As + buf * BM * P::LDS_K, tid);
+    OpB::store(rb, Bs + buf * BN * P::LDS_K, tid);
   };
 
   f32x16 acc[P::TM][P::TN];
@@ -188,14 +211,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool VEC>
+template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool CA, bool CB>
 hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
   using P = GemmBf16<BM, BN, BK, WM, WN>;
-  auto k = gemm_bf16_kernel<BM, BN, BK, WM, WN, VEC>;
+  auto k = gemm_bf16_kernel<BM, BN, BK, WM, WN, VEC, CA, CB>;
   const SplitGeom g = gemm_split_geom(a.K, BK, a.split_k);
   if (g.splits > 1 && P::TM * P::TN * 16 > kSplitMaxAccPerThread) return hipErrorInvalidConfiguration;
   grid.y = (unsigned)g.splits;
-  const size_t lds = GemmBf16<BM, BN, BK, WM, WN>::kLds;
+  const size_t lds = P::kLds;
   static bool attr_set = false;
   if (lds > 65536 && !attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -210,7 +233,7 @@ hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
 
 }  // namespace
 
-template <int BM, int BN, int BK, int NBUF, int WM, int WN>
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB>
 hipError_t launch_gemm_bf16_lds(const MatmulArgs& a);  // gemm_bf16_lds.hip
 
 namespace {
@@ -221,18 +244,43 @@ namespace {
 // above with the same output tile (NBUF == 0: generic kernel only).  Both
 // use the variant's WM x WN waves, so a K split is possible in one exactly
 // when it is in the other.
-template <int BM, int BN, int BK, int NBUF, int WM = 2, int WN = 2>
-hipError_t launch_gemm_bf16(const MatmulArgs& a) {
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB>
+hipError_t launch_layout(const MatmulArgs& a) {
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
   if (tiles == 0) return hipSuccess;
-  const bool vec = (a.K % 8 == 0) && (a.N % 8 == 0) && (a.ldx1 % 8 == 0) && (a.ldx2 % 8 == 0) &&
+  // 16-byte groups of 8 elements never straddle an edge: each operand's
+  // contiguous extent (K, or M / N for the r-contiguous layouts) and both
+  // strides are multiples of 8, and the bases are 16-byte aligned.
+  const int64_t a_run = CA ? a.M : a.K, b_run = CB ? a.K : a.N;
+  const bool vec = (a_run % 8 == 0) && (b_run % 8 == 0) && (a.ldx1 % 8 == 0) && (a.ldx2 % 8 == 0) &&
                    (reinterpret_cast<uintptr_t>(a.x1) % 16 == 0) && (reinterpret_cast<uintptr_t>(a.x2) % 16 == 0);
   if constexpr (NBUF > 0) {
-    if (vec && a.ldx1 < (int64_t(1) << 22) && a.ldx2 < (int64_t(1) << 24))
-      return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN>(a);
+    // The LDS-DMA kernel's byte offsets within one K step: (strided rows of
+    // the tile) * ld * 2 < 2^31 — BM or BN rows for a k-contiguous operand,
+    // BK rows for an r-contiguous one.
+    const int64_t a_rows = CA ? BK : BM, b_rows = CB ? BN : BK;
+    if (vec && a_rows * a.ldx1 * 2 < (int64_t(1) << 31) - 4096 && b_rows * a.ldx2 * 2 < (int64_t(1) << 31) - 4096)
+      return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, CA, CB>(a);
   }
   dim3 grid((unsigned)tiles);
-  return vec ? launch_one<BM, BN, 64, WM, WN, true>(a, grid) : launch_one<BM, BN, 64, WM, WN, false>(a, grid);
+  return vec ? launch_one<BM, BN, 64, WM, WN, true, CA, CB>(a, grid)
+             : launch_one<BM, BN, 64, WM, WN, false, CA, CB>(a, grid);
+}
+
+// Aligned operands (16-byte base, contiguous extents and strides multiples
+// of 8) whose tile offsets fit 32 bits run the LDS-DMA kernel of
+// gemm_bf16_lds.hip with a ring of NBUF stage buffers of BK; everything else
+// runs the generic kernel above with the same output tile (NBUF == 0: generic
+// kernel only).  Both use the variant's WM x WN waves, so a K split is
+// possible in one exactly when it is in the other.
+template <int BM, int BN, int BK, int NBUF, int WM = 2, int WN = 2>
+hipError_t launch_gemm_bf16(const MatmulArgs& a) {
+  switch (a.layout & 3) {
+    case 0: return launch_layout<BM, BN, BK, NBUF, WM, WN, false, false>(a);
+    case TILEC_X1_COL_MAJOR: return launch_layout<BM, BN, BK, NBUF, WM, WN, true, false>(a);
+    case TILEC_X2_COL_MAJOR: return launch_layout<BM, BN, BK, NBUF, WM, WN, false, true>(a);
+    default: return launch_layout<BM, BN, BK, NBUF, WM, WN, true, true>(a);
+  }
 }
 
 }  // namespace

@@ -1,5 +1,6 @@
 // bf16 GEMM for aligned operands, C[M,N] (fp32) = A[M,K] · B[K,N] (bf16,
-// row-major), fp32 accumulate, on v_mfma_f32_32x32x16_bf16.
+// each row- or column-major, read in place), fp32 accumulate, on
+// v_mfma_f32_32x32x16_bf16.
 //
 // Same tile semantics as the reference tile kernel `_matmul_tiled`
 // (tilec/ext.py:13-24): zero accumulator, K steps over masked tiles with
@@ -13,17 +14,19 @@
 //   * The stage buffers are distinct LDS objects and the K loop is unrolled
 //     over the ring, so every access names its buffer statically and the
 //     compiler knows reads of one buffer do not wait on loads into another.
-//   * A lives in LDS row-major (k contiguous) with its 16-byte chunks
-//     XOR-swizzled per row, so the 16-byte operand reads of 16 consecutive
-//     rows hit distinct banks.
-//   * B lives in LDS as it is in memory (n contiguous) and the MFMA B operand
-//     (8 consecutive k of one column per lane) comes from two
+//   * Each operand lives in LDS as it is in memory.  One whose memory runs
+//     along K (row-major A, column-major B) is stored in rows of BK with its
+//     16-byte chunks XOR-swizzled per row, so the 16-byte operand reads of
+//     16 consecutive rows hit distinct banks.  One whose memory runs along M
+//     or N (row-major B, column-major A) is stored in rows of k, and its MFMA
+//     operand (8 consecutive k of one row or column per lane) comes from two
 //     ds_read_b64_tr_b16 transposing reads; chunks of row k are swizzled by
 //     4 * (k & 3) so the 8 rows one read touches spread over the banks.
 //   * Masking is done on addresses: chunks past M, N or K get an out-of-range
 //     buffer offset and land in LDS as zeros.  Operands must be 16-byte
-//     aligned with K, N, lda, ldb multiples of 8 (the launcher checks; other
-//     shapes go to the generic kernel in gemm_bf16.hip).
+//     aligned with contiguous extents and strides multiples of 8 (the
+//     launcher checks; other shapes go to the generic kernel in
+//     gemm_bf16.hip).
 //   * Per K step, the MFMAs of the previous step's last k-slice (read into
 //     registers before the barrier) run right after it, threaded one-for-one
 //     with the next step's loads, so neither the barrier nor the load issue
@@ -42,37 +45,60 @@ typedef short i16x4v __attribute__((ext_vector_type(4)));
 typedef short i16x8v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int BM, int BN, int BK, int NBUF, int WM, int WN>
-struct LdsGemm {
-  static constexpr int NW = WM * WN;
-  static constexpr int NT = NW * 64;
-  static constexpr int WTM = BM / WM, WTN = BN / WN;
-  static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int A_ROW_CHUNKS = BK / 8;  // 16-byte chunks per A row
-  static constexpr int B_ROW_CHUNKS = BN / 8;  // 16-byte chunks per B row
-  static constexpr int A_CHUNKS = BM * A_ROW_CHUNKS;
-  static constexpr int B_CHUNKS = BK * B_ROW_CHUNKS;
-  static constexpr int A_INSTR = A_CHUNKS / 64 / NW;  // DMA instructions per wave per step
-  static constexpr int B_INSTR = B_CHUNKS / 64 / NW;
-  static constexpr int IPS = A_INSTR + B_INSTR;
-  static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
-  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-  static_assert(A_CHUNKS % (64 * NW) == 0 && B_CHUNKS % (64 * NW) == 0, "DMA must divide evenly");
-  static_assert(BN % 128 == 0, "B swizzle needs rows of >= 16 chunks");
-  static_assert(BK == 32 || BK == 64, "A swizzle covers 4 or 8 chunks per row");
-  static_assert(NBUF >= 2 && NBUF <= 4, "ring of 2..4 stage buffers");
-  static_assert((size_t)NBUF * STAGE_BYTES <= 160 * 1024, "LDS is 160 KiB");
-  static_assert((NBUF - 2) * IPS <= 63, "vmcnt is 6 bits");
-};
-
-// A: chunk c of row i is stored at (c ^ swz) within the row; BK=64 rows are
-// 128 B (8 chunks, 2 rows per 256-byte bank line), BK=32 rows 64 B (4 chunks).
+// A k-contiguous stage: chunk c of row i is stored at (c ^ swz_a) within the
+// row; BK=64 rows are 128 B (8 chunks, 2 rows per 256-byte bank line), BK=32
+// rows 64 B (4 chunks).  An r-contiguous stage: chunks of k-row r are
+// swizzled by 4 * (r & 3), so the 8 rows one transposing read touches spread
+// over the banks.
 template <int BK>
 __device__ __forceinline__ int swz_a(int row) {
   return BK == 64 ? (row >> 1) & 7 : (row >> 2) & 3;
 }
 __device__ __forceinline__ int swz_b(int krow) { return 4 * (krow & 3); }
+
+// How one operand's tile (R rows of its outer dimension — M for x1, N for
+// x2 — by BK of K) sits in a stage buffer.
+//   KC (k contiguous in memory: row-major x1, column-major x2): R rows of BK
+//     elements, chunks swizzled by swz_a; an MFMA fragment (8 consecutive k
+//     of one row) is one 16-byte read.
+//   otherwise (r contiguous: row-major x2, column-major x1): BK rows of R
+//     elements, chunks swizzled by swz_b; a fragment comes from two
+//     ds_read_b64_tr_b16 transposing reads.
+template <int R, int BK, int NW, bool KC>
+struct Stage {
+  static constexpr bool kKC = KC;
+  static constexpr int ROW_CHUNKS = KC ? BK / 8 : R / 8;  // 16-byte chunks per stored row
+  static constexpr int CHUNKS = R * BK / 8;
+  static constexpr int INSTR = CHUNKS / 64 / NW;  // DMA instructions per wave per step
+  static constexpr int BYTES = R * BK * 2;
+  static_assert(CHUNKS % (64 * NW) == 0, "DMA must divide evenly");
+  static_assert(KC || R % 128 == 0, "transposed-read swizzle needs rows of >= 16 chunks");
+  static_assert(!KC || BK == 32 || BK == 64, "row swizzle covers 4 or 8 chunks per row");
+  __device__ __forceinline__ static int swz(int row) { return KC ? swz_a<BK>(row) : swz_b(row); }
+  // Stored row and logical chunk of physical chunk p.
+  __device__ __forceinline__ static void chunk(int p, int& row, int& lc) {
+    row = p / ROW_CHUNKS;
+    lc = (p % ROW_CHUNKS) ^ swz(row);
+  }
+};
+
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB>
+struct LdsGemm {
+  static constexpr int NW = WM * WN;
+  static constexpr int NT = NW * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int TM = WTM / 32, TN = WTN / 32;
+  using SA = Stage<BM, BK, NW, !CA>;
+  using SB = Stage<BN, BK, NW, CB>;
+  static constexpr int A_INSTR = SA::INSTR, B_INSTR = SB::INSTR;
+  static constexpr int IPS = A_INSTR + B_INSTR;
+  static constexpr int A_BYTES = SA::BYTES, B_BYTES = SB::BYTES;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+  static_assert(NBUF >= 2 && NBUF <= 4, "ring of 2..4 stage buffers");
+  static_assert((size_t)NBUF * STAGE_BYTES <= 160 * 1024, "LDS is 160 KiB");
+  static_assert((NBUF - 2) * IPS <= 63, "vmcnt is 6 bits");
+};
 
 // s_waitcnt vmcnt(N) with expcnt and lgkmcnt left unconstrained (gfx9
 // encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
@@ -92,12 +118,14 @@ __device__ __forceinline__ void sched_mfma_vmem() {
   }
 }
 
-template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool KFULL>
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool KFULL, bool CA, bool CB>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     const u16* __restrict__ A, const u16* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
     unsigned* __restrict__ counters) {
-  using P = LdsGemm<BM, BN, BK, NBUF, WM, WN>;
+  using P = LdsGemm<BM, BN, BK, NBUF, WM, WN, CA, CB>;
+  using SA = typename P::SA;
+  using SB = typename P::SB;
   constexpr int KS = BK / 16;  // MFMA k-slices per step
   __shared__ int last_flag;
   // The ring: distinct LDS objects (those past NBUF are never referenced).
@@ -128,55 +156,64 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   const int nk = max(0, min((K + BK - 1) / BK, kt0 + split_steps) - kt0);
 
   // ---- global -> LDS for K step kt (local: absolute step kt0 + kt) ----------
-  // Physical chunk p of the A stage holds row p / A_ROW_CHUNKS, logical chunk
-  // (p % A_ROW_CHUNKS) ^ swz_a(row); of the B stage, k-row p / B_ROW_CHUNKS,
-  // logical chunk (p % B_ROW_CHUNKS) ^ swz_b(row).  Instruction i of this
-  // wave fills physical chunks [64 * (wave * INSTR + i), +64), lane l the
-  // l-th of them.  A lane's byte offset from the step's base is the same in
-  // every step; rows past M and columns past N get kOob once, here.  A step
-  // past this workgroup's range gets a resource of zero records, so its
-  // loads touch nothing.  When K % BK != 0 (!KFULL) the last step also masks
-  // A's chunks past K per lane and B's rows past K by the resource's size.
+  // Physical chunk p of an operand's stage area holds stored row
+  // p / ROW_CHUNKS, logical chunk (p % ROW_CHUNKS) ^ swz(row) (Stage).
+  // Instruction i of this wave fills physical chunks [64 * (wave * INSTR +
+  // i), +64), lane l the l-th of them.  A lane's byte offset from the step's
+  // base is the same in every step; chunks past M or N get kOob once, here.
+  // A step past this workgroup's range gets a resource of zero records, so
+  // its loads touch nothing.  When K % BK != 0 (!KFULL) the last step also
+  // masks K: per lane for a k-contiguous operand (its chunk's k column), by
+  // the resource's size for an r-contiguous one (whole stored rows of K).
   uint32_t off_a[P::A_INSTR], off_b[P::B_INSTR];
-  // Column within the A stage of this lane's chunk of instruction i;
-  // recomputed where needed rather than held in registers.
-  auto dma_a_kcol = [&](int i) {
-    const int p = 64 * (wave * P::A_INSTR + i) + lane;
-    const int row = p / P::A_ROW_CHUNKS;
-    return 8 * ((p % P::A_ROW_CHUNKS) ^ swz_a<BK>(row));
+  // The K column of this lane's chunk of instruction i of a k-contiguous
+  // operand; recomputed where needed rather than held in registers.
+  auto kcol = [&](auto st, int i) {
+    using T = decltype(st);
+    int row, lc;
+    T::chunk(64 * (wave * T::INSTR + i) + lane, row, lc);
+    return 8 * lc;
   };
 #pragma unroll
   for (int i = 0; i < P::A_INSTR; ++i) {
-    const int p = 64 * (wave * P::A_INSTR + i) + lane;
-    const int row = p / P::A_ROW_CHUNKS;
-    off_a[i] = m0 + row < M ? 2u * ((uint32_t)row * (uint32_t)lda + (uint32_t)dma_a_kcol(i)) : kOob;
+    int row, lc;
+    SA::chunk(64 * (wave * P::A_INSTR + i) + lane, row, lc);
+    const bool in = CA ? m0 + 8 * lc < M : m0 + row < M;  // stored row = k (CA) or m
+    off_a[i] = in ? 2u * ((uint32_t)row * (uint32_t)lda + 8u * lc) : kOob;
   }
 #pragma unroll
   for (int i = 0; i < P::B_INSTR; ++i) {
-    const int p = 64 * (wave * P::B_INSTR + i) + lane;
-    const int row = p / P::B_ROW_CHUNKS, c = (p % P::B_ROW_CHUNKS) ^ swz_b(row);
-    off_b[i] = n0 + 8 * c < N ? 2u * ((uint32_t)row * (uint32_t)ldb + 8u * c) : kOob;
+    int row, lc;
+    SB::chunk(64 * (wave * P::B_INSTR + i) + lane, row, lc);
+    const bool in = CB ? n0 + row < N : n0 + 8 * lc < N;  // stored row = n (CB) or k
+    off_b[i] = in ? 2u * ((uint32_t)row * (uint32_t)ldb + 8u * lc) : kOob;
   }
+  // Resource of one operand for step k0: based at its tile's first element,
+  // zero records past this workgroup's steps; an r-contiguous operand's K
+  // edge (!KFULL) is the end of its (K - k0)-th stored row.
+  auto op_rsrc = [&](const u16* X, int64_t ld, int r0, bool kcontig, int k0, bool live) {
+    const u16* base = kcontig ? X + (int64_t)r0 * ld + k0 : X + (int64_t)k0 * ld + r0;
+    uint32_t recs = live ? 0x7FFFFFFFu : 0u;
+    if (!KFULL && !kcontig && live) recs = (uint32_t)min<int64_t>((int64_t)(K - k0) * ld * 2, 0x7FFFFFFF);
+    return make_rsrc(base, recs);
+  };
   // Instruction q (0 <= q < IPS) of step kt: A instructions first, then B.
+  // (Offsets are copied out of the arrays before the builtin: passed straight
+  // to it, an array element makes the host pass drop the kernel's stub.)
   auto dma_one = [&](int q, int kt, char* st) __attribute__((always_inline)) {
     const int k0 = (kt0 + kt) * BK;
-    const uint32_t recs = kt < nk ? 0x7FFFFFFFu : 0u;
+    const bool live = kt < nk;
     if (q < P::A_INSTR) {
-      const BufRsrc ra = make_rsrc(A + (int64_t)m0 * lda + k0, recs);
+      const BufRsrc ra = op_rsrc(A, lda, m0, !CA, k0, live);
       uint32_t off = off_a[q];
-      if constexpr (!KFULL) off = k0 + dma_a_kcol(q) < K ? off : kOob;
+      if constexpr (!KFULL && !CA) off = k0 + kcol(SA{}, q) < K ? off : kOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + 16 * 64 * (wave * P::A_INSTR + q)), 16, off, 0,
                                                0, 0);
     } else {
       const int i = q - P::A_INSTR;
-      // B's K edge is the end of whole rows: a resource of (K - k0) rows
-      // masks the rows past it without a per-lane test.
-      uint32_t recs_b = recs;
-      if constexpr (!KFULL) recs_b = kt < nk ? (uint32_t)min<int64_t>((int64_t)(K - k0) * ldb * 2, 0x7FFFFFFF) : 0u;
-      const BufRsrc rb = make_rsrc(B + (int64_t)k0 * ldb + n0, recs_b);
-      // (a copy, not the array element itself: passed straight to the
-      // builtin, the element makes the host pass drop the kernel's stub)
-      const uint32_t off = off_b[i];
+      const BufRsrc rb = op_rsrc(B, ldb, n0, CB, k0, live);
+      uint32_t off = off_b[i];
+      if constexpr (!KFULL && CB) off = k0 + kcol(SB{}, i) < K ? off : kOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(st + P::A_BYTES + 16 * 64 * (wave * P::B_INSTR + i)),
                                                16, off, 0, 0, 0);
     }
@@ -194,24 +231,38 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // Per-lane fragment addressing (bytes within a stage).
+  // Per-lane fragment addressing (bytes within an operand's stage area).
+  // A fragment is 8 consecutive k of one of the wave's 32 rows (MFMA operand
+  // layout: row lane % 32, k-half lane / 32).  From a k-contiguous stage it
+  // is the 16-byte chunk 2 ks + h of that row; from an r-contiguous stage two
+  // transposing reads, of k-rows tr_krow (+4) and 8-row groups holding row
+  // rbase + 16 (g & 1) + 4 (jj & 3), return it.
   const int h = lane >> 5;
   const int g = lane >> 4, jj = lane & 15;
-  int a_row[P::TM];
+  const int tr_row = 16 * (g & 1) + 4 * (jj & 3);
+  const int tr_krow = 8 * (g >> 1) + (jj >> 2);  // + 16 * ks (+ 4 for the second read)
+  int a_r[P::TM];
 #pragma unroll
-  for (int i = 0; i < P::TM; ++i) a_row[i] = wm * P::WTM + 32 * i + (lane & 31);
-  int b_n[P::TN];
+  for (int i = 0; i < P::TM; ++i) a_r[i] = wm * P::WTM + 32 * i + (CA ? tr_row : (lane & 31));
+  int b_r[P::TN];
 #pragma unroll
-  for (int j = 0; j < P::TN; ++j) b_n[j] = wn * P::WTN + 32 * j + 16 * (g & 1) + 4 * (jj & 3);
-  const int b_krow = 8 * (g >> 1) + (jj >> 2);  // + 16 * ks (+ 4 for the second read)
+  for (int j = 0; j < P::TN; ++j) b_r[j] = wn * P::WTN + 32 * j + (CB ? (lane & 31) : tr_row);
 
-  auto a_addr = [&](int i, int ks) {
-    const int row = a_row[i], c = 2 * ks + h;
-    return 16 * (row * P::A_ROW_CHUNKS + (c ^ swz_a<BK>(row)));
-  };
-  auto b_addr = [&](int j, int krow) {
-    const int n = b_n[j];
-    return P::A_BYTES + 16 * (krow * P::B_ROW_CHUNKS + ((n >> 3) ^ swz_b(krow))) + 8 * ((n >> 2) & 1);
+  auto frag = [&](auto st_t, const char* area, int r, int ks) __attribute__((always_inline)) -> bf16x8 {
+    using T = decltype(st_t);
+    if constexpr (T::kKC) {
+      const int c = 2 * ks + h;
+      return *reinterpret_cast<const bf16x8*>(area + 16 * (r * T::ROW_CHUNKS + (c ^ T::swz(r))));
+    } else {
+      auto at = [&](int kr) {
+        return (__attribute__((address_space(3))) i16x4v*)(area + 16 * (kr * T::ROW_CHUNKS + ((r >> 3) ^ T::swz(kr))) +
+                                                          8 * ((r >> 2) & 1));
+      };
+      const int kr = 16 * ks + tr_krow;
+      const i16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(at(kr));
+      const i16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(at(kr + 4));
+      return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
   };
 
   // The operands of one k-slice: A rows of the wave's 32-row blocks, B
@@ -221,14 +272,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   };
   auto read = [&](const char* st, int ks, Frag& f) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < P::TM; ++i) f.a[i] = *reinterpret_cast<const bf16x8*>(st + a_addr(i, ks));
+    for (int i = 0; i < P::TM; ++i) f.a[i] = frag(SA{}, st, a_r[i], ks);
 #pragma unroll
-    for (int j = 0; j < P::TN; ++j) {
-      const int kr = 16 * ks + b_krow;
-      const i16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(st + b_addr(j, kr)));
-      const i16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(st + b_addr(j, kr + 4)));
-      f.b[j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    }
+    for (int j = 0; j < P::TN; ++j) f.b[j] = frag(SB{}, st + P::A_BYTES, b_r[j], ks);
   };
   auto mma = [&](const Frag& f) __attribute__((always_inline)) {
 #pragma unroll
@@ -343,16 +389,17 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
 }  // namespace
 
 // Launch the LDS-DMA kernel; the caller has checked alignment (16-byte
-// operands, K, N, lda, ldb multiples of 8) and the 32-bit offset limits.
-template <int BM, int BN, int BK, int NBUF, int WM, int WN>
+// operands, contiguous extents and strides multiples of 8) and the 32-bit
+// offset limits.
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB>
 hipError_t launch_gemm_bf16_lds(const MatmulArgs& a) {
-  using P = LdsGemm<BM, BN, BK, NBUF, WM, WN>;
+  using P = LdsGemm<BM, BN, BK, NBUF, WM, WN, CA, CB>;
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
   if (tiles == 0) return hipSuccess;
   const SplitGeom g = gemm_split_geom(a.K, BK, a.split_k);
   if (g.splits > 1 && P::TM * P::TN * 16 > kSplitMaxAccPerThread) return hipErrorInvalidConfiguration;
-  auto kern = a.K % BK == 0 ? gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, true>
-                            : gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, false>;
+  auto kern = a.K % BK == 0 ? gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, true, CA, CB>
+                            : gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, false, CA, CB>;
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)g.splits), dim3(P::NT), 0, a.stream,
                      static_cast<const u16*>(a.x1), static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N,
                      (int)a.K, a.ldx1, a.ldx2, a.ldo, 4, (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr,
@@ -360,10 +407,16 @@ hipError_t launch_gemm_bf16_lds(const MatmulArgs& a) {
   return hipGetLastError();
 }
 
-template hipError_t launch_gemm_bf16_lds<256, 256, 32, 4, 2, 2>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<256, 256, 64, 2, 2, 4>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<256, 128, 64, 3, 4, 2>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<256, 128, 32, 4, 2, 2>(const MatmulArgs&);
-template hipError_t launch_gemm_bf16_lds<128, 128, 64, 4, 2, 4>(const MatmulArgs&);
+#define TILEC_LDS_VARIANT(BM, BN, BK, NBUF, WM, WN)                                           \
+  template hipError_t launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, false, false>(const MatmulArgs&); \
+  template hipError_t launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, true, false>(const MatmulArgs&);  \
+  template hipError_t launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, false, true>(const MatmulArgs&);  \
+  template hipError_t launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, true, true>(const MatmulArgs&);
+TILEC_LDS_VARIANT(256, 256, 32, 4, 2, 2)
+TILEC_LDS_VARIANT(256, 256, 64, 2, 2, 4)
+TILEC_LDS_VARIANT(256, 128, 64, 3, 4, 2)
+TILEC_LDS_VARIANT(256, 128, 32, 4, 2, 2)
+TILEC_LDS_VARIANT(128, 128, 64, 4, 2, 4)
+#undef TILEC_LDS_VARIANT
 
 }  // namespace tilec

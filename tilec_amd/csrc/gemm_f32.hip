@@ -1,5 +1,7 @@
 // LDS-staged fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x2f32):
-//   C[M,N] = A[M,K] · B[K,N], fp32 row-major, fp32 accumulate.
+//   C[M,N] = A[M,K] · B[K,N], fp32, fp32 accumulate; C row-major, A and B
+//   each row- or column-major (a column-major operand is read in place:
+//   the transposed view x.T of a contiguous matrix needs no copy).
 //
 // Semantics follow the reference tile kernel `_matmul_tiled`
 // (tilec/ext.py:13-24): one workgroup per BM x BN output tile, an accumulator
@@ -27,19 +29,14 @@ namespace tilec {
 
 namespace {
 
-template <int BM, int BN, int BK, int WM, int WN, bool VEC>
+template <int BM, int BN, int BK, int WM, int WN>
 struct GemmF32 {
   static constexpr int NT = WM * WN * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int LDA_S = BM + 4;  // As[k][m] row length (floats)
-  static constexpr int LDB_S = BN + 4;  // Bs[k][n] row length (floats)
-  static constexpr int A_Q = BM * BK / 4 / NT;  // float4 loads of A per thread
-  static constexpr int B_Q = BK * BN / 4 / NT;  // float4 loads of B per thread
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-  static_assert(BM * BK % (4 * NT) == 0 && BK * BN % (4 * NT) == 0, "tile loads must divide evenly");
   static_assert(BK % 4 == 0 && BK % 2 == 0, "BK");
-  static constexpr size_t kLds = sizeof(float) * 2 * BK * (LDA_S + LDB_S);
+  static constexpr size_t kLds = sizeof(float) * 2 * BK * ((BM + 4) + (BN + 4));
 };
 
 // Four consecutive floats at a 4-byte aligned address: one dwordx4 load,
@@ -63,16 +60,129 @@ __device__ __forceinline__ f32x4 ld4(const float* __restrict__ p, bool ok_all, i
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF>
+// Bytes from p to the end of a matrix of `rows` rows (row stride ld, last
+// row `cols` long), clamped to a buffer's 31-bit range; 0 if none.
+__device__ __forceinline__ uint32_t extent(int64_t rows_left, int64_t ld, int64_t cols_left) {
+  if (rows_left <= 0 || cols_left <= 0) return 0u;
+  const int64_t bytes = 4 * ((rows_left - 1) * ld + cols_left);
+  return bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)bytes;
+}
+
+// One operand's tile per K step: R rows of the operand's outer dimension (M
+// for x1, N for x2) by BK of K, moved global -> registers -> LDS.  KC: the
+// operand's element (r, k) is X[r * ld + k] (k contiguous: row-major x1,
+// column-major x2); otherwise X[k * ld + r] (r contiguous: row-major x2,
+// column-major x1).  Each thread moves Q quads of 4 elements contiguous in
+// memory.  In LDS the tile is S[k][r] with rows of R + 4 floats, the layout
+// the MFMA operand reads expect for either operand.
+template <int R, int BK, int NT, bool KC, bool VEC, bool BUF>
+struct OperandF32 {
+  static constexpr int Q = R * BK / 4 / NT;
+  static constexpr int LDS_S = R + 4;
+  static_assert(R * BK % (4 * NT) == 0, "tile loads must divide evenly");
+  const float* X;
+  int64_t ld;
+  int r0, Rtot, K;
+  int tr[Q], tk[Q], rvalid[Q];
+  uint32_t off[Q];
+  f32x4 v[Q];
+
+  // Tile row and tile k of the first element of quad e.
+  __device__ __forceinline__ static void coord(int e, int& r, int& k) {
+    if constexpr (KC) {
+      r = e / (BK / 4);
+      k = 4 * (e % (BK / 4));
+    } else {
+      k = e / (R / 4);
+      r = 4 * (e % (R / 4));
+    }
+  }
+
+  __device__ __forceinline__ void init(const float* X_, int64_t ld_, int r0_, int Rtot_, int K_, int tid) {
+    X = X_;
+    ld = ld_;
+    r0 = r0_;
+    Rtot = Rtot_;
+    K = K_;
+#pragma unroll
+    for (int p = 0; p < Q; ++p) {
+      coord(tid + p * NT, tr[p], tk[p]);
+      if constexpr (BUF) {
+        // The outer dimension's edge is fixed per tile: quads past it get kOob
+        // once; K's edge moves with the step.
+        if constexpr (KC) {
+          rvalid[p] = r0 + tr[p] < Rtot ? 4 : 0;
+          off[p] = rvalid[p] ? 4u * ((uint32_t)tr[p] * (uint32_t)ld + (uint32_t)tk[p]) : kOob;
+        } else {
+          rvalid[p] = max(0, min(4, Rtot - (r0 + tr[p])));
+          off[p] = rvalid[p] > 0 ? 4u * ((uint32_t)tk[p] * (uint32_t)ld + (uint32_t)tr[p]) : kOob;
+        }
+      }
+    }
+  }
+
+  // Global -> registers for K step kt.  BUF: a resource that ends at the
+  // matrix's last element, out-of-range offsets for masked quads, and (when
+  // !VEC) a select that clears the columns past the edge inside the quad that
+  // straddles it.  Otherwise MASK selects clamped, per-element loads at
+  // every edge and unmasked 16-byte loads elsewhere.
+  __device__ __forceinline__ void load(int kt, bool mask) {
+    const int k0 = kt * BK;
+    if constexpr (BUF) {
+      const BufRsrc rs = KC ? make_rsrc(X + (int64_t)r0 * ld + k0, extent(Rtot - r0, ld, K - k0))
+                            : make_rsrc(X + (int64_t)k0 * ld + r0, extent(K - k0, ld, Rtot - r0));
+#pragma unroll
+      for (int p = 0; p < Q; ++p) {
+        f32x4 x = load_f32x4(rs, k0 + tk[p] < K ? off[p] : kOob);
+        if constexpr (!VEC) {
+          const int valid = KC ? K - (k0 + tk[p]) : rvalid[p];
+#pragma unroll
+          for (int c = 1; c < 4; ++c) x[c] = c < valid ? x[c] : 0.f;
+        }
+        v[p] = x;
+      }
+      return;
+    }
+#pragma unroll
+    for (int p = 0; p < Q; ++p) {
+      const int gr = r0 + tr[p], gk = k0 + tk[p];
+      const int64_t at = KC ? (int64_t)gr * ld + gk : (int64_t)gk * ld + gr;
+      if (!mask) {  // whole quad in bounds: one (dword-aligned) 16-byte load
+        v[p] = *reinterpret_cast<const f32x4_a4*>(X + at);
+      } else {
+        const int valid = KC ? (gr < Rtot ? max(0, min(4, K - gk)) : 0) : (gk < K ? max(0, min(4, Rtot - gr)) : 0);
+        v[p] = ld4<VEC>(X + (valid > 0 ? at : 0), valid == 4, valid);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* __restrict__ S) const {
+#pragma unroll
+    for (int p = 0; p < Q; ++p) {
+      if constexpr (KC) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) S[(tk[p] + c) * LDS_S + tr[p]] = v[p][c];
+      } else {
+        *reinterpret_cast<f32x4*>(S + tk[p] * LDS_S + tr[p]) = v[p];
+      }
+    }
+  }
+};
+
+// CA: x1 is column-major (element (m, k) at A[m + k * lda]); CB: x2 is
+// column-major (element (k, n) at B[k + n * ldb]).
+template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF, bool CA, bool CB>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
     unsigned* __restrict__ counters) {
-  using P = GemmF32<BM, BN, BK, WM, WN, VEC>;
+  using P = GemmF32<BM, BN, BK, WM, WN>;
+  using OpA = OperandF32<BM, BK, P::NT, !CA, VEC, BUF>;
+  using OpB = OperandF32<BN, BK, P::NT, CB, VEC, BUF>;
   extern __shared__ __align__(16) float lds[];
   __shared__ int last_flag;
-  float* As = lds;                          // [2][BK][LDA_S]
-  float* Bs = lds + 2 * BK * P::LDA_S;      // [2][BK][LDB_S]
+  float* As = lds;                          // [2][BK][BM + 4]
+  float* Bs = lds + 2 * BK * OpA::LDS_S;    // [2][BK][BN + 4]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -88,114 +198,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
   const int kt1 = min((K + BK - 1) / BK, kt0 + split_steps);
   const int nk_full = K / BK;
 
-  f32x4 ra[P::A_Q], rb[P::B_Q];
-
-  // BUF: per-thread quad coordinates are fixed for the whole K loop; the
-  // resources move with k0.  Columns a quad keeps: A's K edge moves with the
-  // step, B's N edge is fixed per tile.
-  int a_row[P::A_Q], a_k[P::A_Q], b_k[P::B_Q], b_valid[P::B_Q];
-  uint32_t a_off[P::A_Q], b_off[P::B_Q];
-  if constexpr (BUF) {
-#pragma unroll
-    for (int p = 0; p < P::A_Q; ++p) {
-      const int e = tid + p * P::NT;
-      a_row[p] = e / (BK / 4);
-      a_k[p] = 4 * (e % (BK / 4));
-      a_off[p] = m0 + a_row[p] < M ? 4u * ((uint32_t)a_row[p] * (uint32_t)lda + (uint32_t)a_k[p]) : kOob;
-    }
-#pragma unroll
-    for (int p = 0; p < P::B_Q; ++p) {
-      const int e = tid + p * P::NT;
-      b_k[p] = e / (BN / 4);
-      const int n = 4 * (e % (BN / 4));
-      b_valid[p] = max(0, min(4, N - (n0 + n)));
-      b_off[p] = b_valid[p] > 0 ? 4u * ((uint32_t)b_k[p] * (uint32_t)ldb + (uint32_t)n) : kOob;
-    }
-  }
-  // Bytes from p to the end of a matrix of `rows` rows (row stride ld, last
-  // row `cols` long), clamped to a buffer's 31-bit range; 0 if none.
-  auto extent = [](int64_t rows_left, int64_t ld, int64_t cols_left) -> uint32_t {
-    if (rows_left <= 0 || cols_left <= 0) return 0u;
-    const int64_t bytes = 4 * ((rows_left - 1) * ld + cols_left);
-    return bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)bytes;
-  };
-  auto gload_buf = [&](int kt) {
-    const int k0 = kt * BK;
-    const BufRsrc rA = make_rsrc(A + (int64_t)m0 * lda + k0, extent(M - m0, lda, K - k0));
-    const BufRsrc rB = make_rsrc(B + (int64_t)k0 * ldb + n0, extent(K - k0, ldb, N - n0));
-#pragma unroll
-    for (int p = 0; p < P::A_Q; ++p) {
-      f32x4 v = load_f32x4(rA, k0 + a_k[p] < K ? a_off[p] : kOob);
-      if constexpr (!VEC) {
-        const int valid = K - (k0 + a_k[p]);
-#pragma unroll
-        for (int c = 1; c < 4; ++c) v[c] = c < valid ? v[c] : 0.f;
-      }
-      ra[p] = v;
-    }
-#pragma unroll
-    for (int p = 0; p < P::B_Q; ++p) {
-      f32x4 v = load_f32x4(rB, k0 + b_k[p] < K ? b_off[p] : kOob);
-      if constexpr (!VEC) {
-#pragma unroll
-        for (int c = 1; c < 4; ++c) v[c] = c < b_valid[p] ? v[c] : 0.f;
-      }
-      rb[p] = v;
-    }
-  };
-
-  // Global -> registers for K tile kt.  MASK: clamp + select at every edge.
+  OpA opa;
+  OpB opb;
+  opa.init(A, lda, m0, M, K, tid);
+  opb.init(B, ldb, n0, N, K, tid);
   auto gload = [&](int kt, bool mask) {
-    if constexpr (BUF) {
-      gload_buf(kt);
-      return;
-    }
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int p = 0; p < P::A_Q; ++p) {
-      const int e = tid + p * P::NT;
-      const int i = e / (BK / 4), kq = e % (BK / 4);
-      const int gm = m0 + i, gk = k0 + 4 * kq;
-      if (!mask) {  // whole quad in bounds: one (dword-aligned) 16-byte load
-        ra[p] = *reinterpret_cast<const f32x4_a4*>(A + (int64_t)gm * lda + gk);
-      } else {
-        const bool rok = gm < M;
-        const int valid = rok ? max(0, min(4, K - gk)) : 0;
-        const int64_t off = valid > 0 ? (int64_t)gm * lda + gk : 0;
-        ra[p] = ld4<VEC>(A + off, valid == 4, valid);
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < P::B_Q; ++p) {
-      const int e = tid + p * P::NT;
-      const int k = e / (BN / 4), jq = e % (BN / 4);
-      const int gk = k0 + k, gn = n0 + 4 * jq;
-      if (!mask) {
-        rb[p] = *reinterpret_cast<const f32x4_a4*>(B + (int64_t)gk * ldb + gn);
-      } else {
-        const int valid = gk < K ? max(0, min(4, N - gn)) : 0;
-        const int64_t off = valid > 0 ? (int64_t)gk * ldb + gn : 0;
-        rb[p] = ld4<VEC>(B + off, valid == 4, valid);
-      }
-    }
+    opa.load(kt, mask);
+    opb.load(kt, mask);
   };
-
   auto sstore = [&](int buf) {
-    float* as = As + buf * BK * P::LDA_S;
-    float* bs = Bs + buf * BK * P::LDB_S;
-#pragma unroll
-    for (int p = 0; p < P::A_Q; ++p) {
-      const int e = tid + p * P::NT;
-      const int i = e / (BK / 4), kq = e % (BK / 4);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) as[(4 * kq + c) * P::LDA_S + i] = ra[p][c];
-    }
-#pragma unroll
-    for (int p = 0; p < P::B_Q; ++p) {
-      const int e = tid + p * P::NT;
-      const int k = e / (BN / 4), jq = e % (BN / 4);
-      *reinterpret_cast<f32x4*>(bs + k * P::LDB_S + 4 * jq) = rb[p];
-    }
+    opa.store(As + buf * BK * OpA::LDS_S);
+    opb.store(Bs + buf * BK * OpB::LDS_S);
   };
 
   f32x16 acc[P::TM][P::TN];
@@ -220,16 +233,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     const int buf = (kt - kt0) & 1;
     const bool more = kt + 1 < kt1;
     if (more) gload(kt + 1, !(interior && kt + 1 < nk_full));
-    const float* as = As + buf * BK * P::LDA_S;
-    const float* bs = Bs + buf * BK * P::LDB_S;
+    const float* as = As + buf * BK * OpA::LDS_S;
+    const float* bs = Bs + buf * BK * OpB::LDS_S;
 #pragma unroll
     for (int ks = 0; ks < BK / 2; ++ks) {
       const int k = 2 * ks + khalf;
       float a[P::TM], b[P::TN];
 #pragma unroll
-      for (int i = 0; i < P::TM; ++i) a[i] = as[k * P::LDA_S + arow + 32 * i];
+      for (int i = 0; i < P::TM; ++i) a[i] = as[k * OpA::LDS_S + arow + 32 * i];
 #pragma unroll
-      for (int j = 0; j < P::TN; ++j) b[j] = bs[k * P::LDB_S + bcol + 32 * j];
+      for (int j = 0; j < P::TN; ++j) b[j] = bs[k * OpB::LDS_S + bcol + 32 * j];
 #pragma unroll
       for (int i = 0; i < P::TM; ++i)
 #pragma unroll
@@ -258,14 +271,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF>
+template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF, bool CA, bool CB>
 hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
-  using P = GemmF32<BM, BN, BK, WM, WN, VEC>;
-  auto k = gemm_f32_kernel<BM, BN, BK, WM, WN, VEC, BUF>;
+  using P = GemmF32<BM, BN, BK, WM, WN>;
+  auto k = gemm_f32_kernel<BM, BN, BK, WM, WN, VEC, BUF, CA, CB>;
   const SplitGeom g = gemm_split_geom(a.K, BK, a.split_k);
   if (g.splits > 1 && P::TM * P::TN * 16 > kSplitMaxAccPerThread) return hipErrorInvalidConfiguration;
   grid.y = (unsigned)g.splits;
-  const size_t lds = GemmF32<BM, BN, BK, WM, WN, VEC>::kLds;
+  const size_t lds = P::kLds;
   static bool attr_set = false;
   if (lds > 65536 && !attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -278,19 +291,38 @@ hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
-hipError_t launch_gemm_f32(const MatmulArgs& a) {
+template <int BM, int BN, int BK, int WM, int WN, bool CA, bool CB>
+hipError_t launch_layout(const MatmulArgs& a) {
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
   if (tiles == 0) return hipSuccess;
-  const bool vec = (a.K % 4 == 0) && (a.N % 4 == 0) && (a.ldx1 % 4 == 0) && (a.ldx2 % 4 == 0) &&
+  // 16-byte quads never straddle an edge: the contiguous extent of each
+  // operand (K, or M / N for the r-contiguous layouts) and both strides are
+  // multiples of 4, and the bases are 16-byte aligned.
+  const int64_t a_run = CA ? a.M : a.K, b_run = CB ? a.K : a.N;
+  const bool vec = (a_run % 4 == 0) && (b_run % 4 == 0) && (a.ldx1 % 4 == 0) && (a.ldx2 % 4 == 0) &&
                    (reinterpret_cast<uintptr_t>(a.x1) % 16 == 0) && (reinterpret_cast<uintptr_t>(a.x2) % 16 == 0);
-  // Buffer offsets inside one K step: row * ld * 4 + 16 * quad < 2^31.
-  const bool buf = (int64_t)BM * a.ldx1 * 4 + 4 * BK < (int64_t(1) << 31) &&
-                   (int64_t)BK * a.ldx2 * 4 + 4 * BN < (int64_t(1) << 31);
+  // Buffer offsets inside one K step: (strided rows of the tile) * ld * 4 +
+  // one row's span < 2^31.
+  const int64_t a_rows = CA ? BK : BM, a_span = CA ? BM : BK;
+  const int64_t b_rows = CB ? BN : BK, b_span = CB ? BK : BN;
+  const bool buf = a_rows * a.ldx1 * 4 + 4 * a_span < (int64_t(1) << 31) &&
+                   b_rows * a.ldx2 * 4 + 4 * b_span < (int64_t(1) << 31);
   dim3 grid((unsigned)tiles);
   if (buf)
-    return vec ? launch_one<BM, BN, BK, WM, WN, true, true>(a, grid) : launch_one<BM, BN, BK, WM, WN, false, true>(a, grid);
-  return vec ? launch_one<BM, BN, BK, WM, WN, true, false>(a, grid) : launch_one<BM, BN, BK, WM, WN, false, false>(a, grid);
+    return vec ? launch_one<BM, BN, BK, WM, WN, true, true, CA, CB>(a, grid)
+               : launch_one<BM, BN, BK, WM, WN, false, true, CA, CB>(a, grid);
+  return vec ? launch_one<BM, BN, BK, WM, WN, true, false, CA, CB>(a, grid)
+             : launch_one<BM, BN, BK, WM, WN, false, false, CA, CB>(a, grid);
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+hipError_t launch_gemm_f32(const MatmulArgs& a) {
+  switch (a.layout & 3) {
+    case 0: return launch_layout<BM, BN, BK, WM, WN, false, false>(a);
+    case TILEC_X1_COL_MAJOR: return launch_layout<BM, BN, BK, WM, WN, true, false>(a);
+    case TILEC_X2_COL_MAJOR: return launch_layout<BM, BN, BK, WM, WN, false, true>(a);
+    default: return launch_layout<BM, BN, BK, WM, WN, true, true>(a);
+  }
 }
 
 }  // namespace

@@ -29,7 +29,21 @@
 // 4 KiB of x2 a wave issues 16 MFMAs for fp32 (512 cycles, 2.5x the rate the
 // HBM share of a SIMD needs) and 32 for bf16 (1.25x), for any M <= 16.
 //
-// Grid: x = 64-column slabs, y = K splits, z = 16-row blocks of x1 and out.
+// Column-major x2 (x @ W.T with W [N, K] row-major, read in place): a
+// column of x2 is a contiguous run of K, so a block is the slab's 16*CPL
+// columns by 4 E consecutive k (E = 4 fp32 or 8 bf16 per 16 bytes): lane l
+// loads columns 16g + q (g < CPL) at k = E*r .. E*r + E-1 and x1[q][E*r ..].
+// That is the MFMA A operand with x2's columns as its rows (A[i=q][k]) and
+// x1 as the B operand (B[k][j=q]), so D_g[n][m] accumulates out^T; bf16
+// needs no widening here, the 8 consecutive k of a lane being exactly the
+// v_mfma_f32_16x16x32_bf16 operand.  Lane l then holds out[q][16g + 4r ..
+// 16g + 4r + 3], which is one float4 item of the same LDS reduction.  A wave
+// load covers 16 columns x 64 bytes; the waves' interleaved blocks make up
+// contiguous runs.  Column-major x1 is read element by element (it is small
+// and cache-resident).
+//
+// Grid: x = slabs of 16*CPL columns, y = K splits, z = 16-row blocks of x1
+// and out.
 // Waves are summed through LDS; with a split K each workgroup writes its
 // [16 x SLAB] partial to the workspace, and the last workgroup of a (row
 // block, slab) to finish (completion counter) adds the partials in split
@@ -43,7 +57,7 @@ namespace tilec {
 namespace {
 
 constexpr int kMaxM = 16;      // MFMA rows
-constexpr int kBlock = 16;     // x2 rows per block (4 MFMA steps of 4 rows)
+constexpr int kBlock = 16;     // K chunks are whole multiples of 16 rows
 constexpr int kKcMax = 1024;   // rows per K chunk at most
 constexpr int kCounterStride = 64;  // uint32s between completion counters (own 256-byte line each)
 
@@ -51,27 +65,53 @@ typedef unsigned short u16;  // bf16 bit pattern
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 // Element type: CPL columns per 16-byte row load, slab = 16 * CPL columns,
-// NQ = CPL / 4 output float4 per lane and row.
+// NQ = CPL / 4 output float4 per lane and row, E elements per 16 bytes.
 template <typename T>
 struct Elem;
 template <>
 struct Elem<float> {
   static constexpr int CPL = 4, BYTES = 4;
-  struct Block {  // one 16-row block: x2 rows 4r+u, x1[q][4r .. 4r+3]
-    f32x4 b[4];
-    f32x4 a;
-  };
 };
 template <>
 struct Elem<u16> {
   static constexpr int CPL = 8, BYTES = 2;
-  struct Block {  // the same, as raw bf16 pairs (low half = lower column / k)
-    i32x4 b[4];
-    i32x2 a;
-  };
 };
 template <typename T>
 constexpr int kSlabOf = 16 * Elem<T>::CPL;
+
+// One block of a wave's share of x2 and the x1 values it multiplies.
+//   x2 row-major (CB = false): x2 rows 4r + u (u < 4), CPL columns each, and
+//     x1[q][4r .. 4r+3]; the block covers 16 rows of K.
+//   x2 column-major (CB = true): columns 16g + q (g < CPL) of x2, E
+//     consecutive k each (k = E*r ..), and x1[q][E*r .. E*r + E-1]; the block
+//     covers 4E rows of K.
+// bf16 values are kept as raw pairs (low half = lower column / k).
+template <typename T, bool CB>
+struct Blk;
+template <>
+struct Blk<float, false> {
+  static constexpr int KB = 16;
+  f32x4 b[4];
+  f32x4 a;
+};
+template <>
+struct Blk<u16, false> {
+  static constexpr int KB = 16;
+  i32x4 b[4];
+  i32x2 a;
+};
+template <>
+struct Blk<float, true> {
+  static constexpr int KB = 16;
+  f32x4 b[4];
+  f32x4 a;
+};
+template <>
+struct Blk<u16, true> {
+  static constexpr int KB = 32;
+  i32x4 b[8];
+  i32x4 a;
+};
 
 __device__ __forceinline__ float bf16_lo(int w) { return __int_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(int w) { return __int_as_float(w & (int)0xffff0000u); }
@@ -109,14 +149,16 @@ __device__ __forceinline__ void store_quad(float* __restrict__ row, int col, int
   }
 }
 
-template <typename T, int WAVES, int UB, bool VEC>
+template <typename T, int WAVES, int UB, bool VEC, bool CA, bool CB>
 __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
     const T* __restrict__ x1, const T* __restrict__ x2, float* __restrict__ out,
     int M_all, int N, int K, int64_t ldx1, int64_t ldx2, int64_t ldo, int kc,
     unsigned* __restrict__ counters, float* __restrict__ part) {
   using E = Elem<T>;
-  using Block = typename E::Block;
+  using Block = Blk<T, CB>;
   constexpr int CPL = E::CPL, NQ = CPL / 4, SLAB = kSlabOf<T>, NT = WAVES * 64;
+  constexpr int EPL = 16 / E::BYTES;  // elements per 16-byte load
+  constexpr int KB = Block::KB;       // rows of K per block
   constexpr uint32_t EB = E::BYTES;
   __shared__ f32x4 red[WAVES * kMaxM * 16 * NQ];  // [wave][row][lane column group q][h]
   __shared__ int last_flag;
@@ -129,62 +171,108 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
   const int nslabs = gridDim.x, S = gridDim.y;
   // This workgroup's row block: rows 16*rb .. of x1 and out, M of them.
   const int M = min(kMaxM, M_all - kMaxM * rb);
-  x1 += (int64_t)kMaxM * rb * ldx1;
+  x1 += CA ? (int64_t)kMaxM * rb : (int64_t)kMaxM * rb * ldx1;
   out += (int64_t)kMaxM * rb * ldo;
   const int cell = rb * nslabs + slab;  // (row block, slab): partial slot and counter
-  const int col = slab * SLAB + CPL * q;
+  const int n0 = slab * SLAB;
+  const int col = n0 + CPL * q;
   const bool col_ok = col < N;
   const int kbeg = split * kc;
   const int nrows = max(0, min(K, kbeg + kc) - kbeg);
-  const int nblocks = (nrows + kBlock - 1) / kBlock;
+  const int nblocks = (nrows + KB - 1) / KB;
 
-  // Block b covers rows kbeg + 16b .. +15.  Resources are based at the
-  // block, so byte offsets stay small (host checks ldx1, ldx2 < 2^25).
+  // Block b covers rows kbeg + KB*b .. of K.  Resources are based at the
+  // block, so byte offsets stay small (the host bounds ldx1 and ldx2).
   // Every mask is an out-of-range offset: the loaded registers feed the
   // MFMAs directly, and a block past the chunk is all zeros (A and B).
   const uint32_t col_off = EB * (uint32_t)col;
-  const uint32_t a_off = EB * ((uint32_t)q * (uint32_t)ldx1 + 4u * (uint32_t)r);
   const bool a_row = q < M;
-  auto load_block = [&](int b, Block& blk) __attribute__((always_inline)) {
-    const int brow = 16 * b;  // wave-uniform, relative to kbeg
-    const BufRsrc rx2 = make_rsrc(x2 + (int64_t)(kbeg + brow) * ldx2);
-    const BufRsrc rx1 = make_rsrc(x1 + kbeg + brow);
+  // x1 element (row q, k = kbeg + brow + kr) of this lane: 0 if masked.
+  auto x1_off = [&](int brow, int kr) -> uint32_t {
+    if (!(a_row & (brow + kr < nrows))) return kOob;
+    return CA ? EB * ((uint32_t)kr * (uint32_t)ldx1 + (uint32_t)q) : EB * ((uint32_t)q * (uint32_t)ldx1 + (uint32_t)kr);
+  };
+  auto x1_rsrc = [&](int brow) {
+    return make_rsrc(CA ? x1 + (int64_t)(kbeg + brow) * ldx1 : x1 + kbeg + brow);
+  };
+  // Dword w of a 16-byte group from its elements' bit patterns h[].
+  auto pack = [](const int* h, int w) -> int { return E::BYTES == 4 ? h[w] : (h[2 * w] | (h[2 * w + 1] << 16)); };
+  auto put = [&](auto& v, const int* h) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int row = 4 * r + u;
-      const bool ok = brow + row < nrows;
-      const uint32_t roff = EB * (uint32_t)row * (uint32_t)ldx2;
-      if constexpr (VEC) {
-        const uint32_t o = (ok & col_ok) ? roff + col_off : kOob;
-        if constexpr (CPL == 4) blk.b[u] = load_f32x4(rx2, o);
-        else blk.b[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, 0));
-      } else if constexpr (CPL == 4) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          blk.b[u][c] = load_f32(rx2, (ok & (col + c < N)) ? roff + col_off + 4u * c : kOob);
-      } else {
-        u16 h[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-          h[c] = __builtin_amdgcn_raw_buffer_load_b16(rx2, (int)((ok & (col + c < N)) ? roff + col_off + 2u * c : kOob), 0, 0);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) blk.b[u][w] = (int)h[2 * w] | ((int)h[2 * w + 1] << 16);
-      }
+    for (int w = 0; w < 4; ++w) {
+      if constexpr (E::BYTES == 4) v[w] = __builtin_bit_cast(float, pack(h, w));
+      else v[w] = pack(h, w);
     }
-    if constexpr (VEC) {  // K % 4 == 0: the 4 k of a lane are all valid or all past the chunk
-      const uint32_t o = (a_row & (brow + 4 * r < nrows)) ? a_off : kOob;
-      if constexpr (CPL == 4) blk.a = load_f32x4(rx1, o);
-      else blk.a = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(rx1, (int)o, 0, 0));
-    } else if constexpr (CPL == 4) {
+  };
+  auto ld_elem = [&](const BufRsrc& rs, uint32_t o) -> int {
+    if constexpr (E::BYTES == 4) return __builtin_bit_cast(int, load_f32(rs, o));
+    else return (int)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)o, 0, 0);
+  };
+  auto load_block = [&](int b, Block& blk) __attribute__((always_inline)) {
+    const int brow = KB * b;  // wave-uniform, relative to kbeg
+    const BufRsrc rx1 = x1_rsrc(brow);
+    if constexpr (!CB) {
+      const BufRsrc rx2 = make_rsrc(x2 + (int64_t)(kbeg + brow) * ldx2);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) blk.a[u] = load_f32(rx1, (a_row & (brow + 4 * r + u < nrows)) ? a_off + 4u * u : kOob);
+      for (int u = 0; u < 4; ++u) {
+        const int row = 4 * r + u;
+        const bool ok = brow + row < nrows;
+        const uint32_t roff = EB * (uint32_t)row * (uint32_t)ldx2;
+        if constexpr (VEC) {
+          const uint32_t o = (ok & col_ok) ? roff + col_off : kOob;
+          if constexpr (CPL == 4) blk.b[u] = load_f32x4(rx2, o);
+          else blk.b[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, 0));
+        } else {
+          int h[CPL];
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) h[c] = ld_elem(rx2, (ok & (col + c < N)) ? roff + col_off + EB * c : kOob);
+          put(blk.b[u], h);
+        }
+      }
+      // x1[q][4r .. 4r+3]
+      if constexpr (VEC && !CA) {  // K % 4 == 0: the 4 k of a lane are all valid or all past the chunk
+        const uint32_t o = x1_off(brow, 4 * r);
+        if constexpr (CPL == 4) blk.a = load_f32x4(rx1, o);
+        else blk.a = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(rx1, (int)o, 0, 0));
+      } else {
+        int h[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) h[u] = ld_elem(rx1, x1_off(brow, 4 * r + u));
+        if constexpr (CPL == 4) {
+          put(blk.a, h);
+        } else {
+          blk.a[0] = h[0] | (h[1] << 16);
+          blk.a[1] = h[2] | (h[3] << 16);
+        }
+      }
     } else {
-      u16 h[4];
+      // x2 column-major: columns n0 + 16g + q, k = kbeg + brow + EPL*r ..
+      const BufRsrc rx2 = make_rsrc(x2 + (int64_t)n0 * ldx2 + kbeg + brow);
+      const int kr = EPL * r;
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        h[u] = __builtin_amdgcn_raw_buffer_load_b16(rx1, (int)((a_row & (brow + 4 * r + u < nrows)) ? a_off + 2u * u : kOob), 0, 0);
-      blk.a[0] = (int)h[0] | ((int)h[1] << 16);
-      blk.a[1] = (int)h[2] | ((int)h[3] << 16);
+      for (int g = 0; g < CPL; ++g) {
+        const int n = 16 * g + q;
+        const bool nok = n0 + n < N;
+        const uint32_t noff = EB * ((uint32_t)n * (uint32_t)ldx2 + (uint32_t)kr);
+        if constexpr (VEC) {  // K % EPL == 0: a lane's EPL k are all valid or all past the chunk
+          const uint32_t o = (nok & (brow + kr < nrows)) ? noff : kOob;
+          blk.b[g] = __builtin_bit_cast(decltype(blk.a), __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, 0));
+        } else {
+          int h[EPL];
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) h[e] = ld_elem(rx2, (nok & (brow + kr + e < nrows)) ? noff + EB * e : kOob);
+          put(blk.b[g], h);
+        }
+      }
+      // x1[q][kr .. kr + EPL-1]
+      if constexpr (VEC && !CA) {
+        blk.a = __builtin_bit_cast(decltype(blk.a), __builtin_amdgcn_raw_buffer_load_b128(rx1, (int)x1_off(brow, kr), 0, 0));
+      } else {
+        int h[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) h[e] = ld_elem(rx1, x1_off(brow, kr + e));
+        put(blk.a, h);
+      }
     }
   };
 
@@ -192,18 +280,33 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
 #pragma unroll
   for (int c = 0; c < CPL; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto mma_block = [&](const Block& blk) __attribute__((always_inline)) {
+    if constexpr (!CB) {
+      // D_c[m][q] += sum_r x1[m][4r+u] * x2[4r+u][col + c]
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      float a;
-      if constexpr (CPL == 4) a = blk.a[u];
-      else a = (u & 1) ? bf16_hi(blk.a[u >> 1]) : bf16_lo(blk.a[u >> 1]);
+      for (int u = 0; u < 4; ++u) {
+        float a;
+        if constexpr (CPL == 4) a = blk.a[u];
+        else a = (u & 1) ? bf16_hi(blk.a[u >> 1]) : bf16_lo(blk.a[u >> 1]);
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        float b;
-        if constexpr (CPL == 4) b = blk.b[u][c];
-        else b = (c & 1) ? bf16_hi(blk.b[u][c >> 1]) : bf16_lo(blk.b[u][c >> 1]);
-        acc[c] = mfma16x16x4(a, b, acc[c]);
+        for (int c = 0; c < CPL; ++c) {
+          float b;
+          if constexpr (CPL == 4) b = blk.b[u][c];
+          else b = (c & 1) ? bf16_hi(blk.b[u][c >> 1]) : bf16_lo(blk.b[u][c >> 1]);
+          acc[c] = mfma16x16x4(a, b, acc[c]);
+        }
       }
+    } else if constexpr (CPL == 4) {
+      // D_g[n][m] += sum_r x2[4r+c][n0 + 16g + n] * x1[m][4r+c]: x2's column
+      // block is the A operand (A[i=q][k=r]), x1 the B operand (B[k=r][j=q]).
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[g] = mfma16x16x4(blk.b[g][c], blk.a[c], acc[g]);
+    } else {
+      // bf16: 8 consecutive k per lane is the 16x16x32 bf16 operand layout.
+#pragma unroll
+      for (int g = 0; g < CPL; ++g)
+        acc[g] = mfma16x16x32bf16(__builtin_bit_cast(bf16x8, blk.b[g]), __builtin_bit_cast(bf16x8, blk.a), acc[g]);
     }
   };
 
@@ -240,13 +343,23 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
     for (int j = 0; j < UB; ++j) mma_block(A[j]);
   }
 
-  // Lane l holds D_c[4r + v][q] in acc[c][v]: out row 4r+v, column col + c.
+  // Item (row m, column group q, half h) holds out[m][n0 + CPL*q + 4h .. +3].
+  if constexpr (!CB) {
+    // Lane l holds D_c[4r + v][q] in acc[c][v]: out row 4r+v, column col + c.
 #pragma unroll
-  for (int v = 0; v < 4; ++v)
+    for (int v = 0; v < 4; ++v)
 #pragma unroll
-    for (int h = 0; h < NQ; ++h)
-      red[((wave * kMaxM + 4 * r + v) * 16 + q) * NQ + h] =
-          f32x4{acc[4 * h][v], acc[4 * h + 1][v], acc[4 * h + 2][v], acc[4 * h + 3][v]};
+      for (int h = 0; h < NQ; ++h)
+        red[((wave * kMaxM + 4 * r + v) * 16 + q) * NQ + h] =
+            f32x4{acc[4 * h][v], acc[4 * h + 1][v], acc[4 * h + 2][v], acc[4 * h + 3][v]};
+  } else {
+    // Lane l holds D_g[4r + v][q] in acc[g][v]: out row q, column n0 + 16g + 4r + v.
+#pragma unroll
+    for (int g = 0; g < CPL; ++g) {
+      const int c = 16 * g + 4 * r;
+      red[((wave * kMaxM + q) * 16 + c / CPL) * NQ + (c % CPL) / 4] = acc[g];
+    }
+  }
   __syncthreads();
 
   // Output items: (row m, column group q, half h) -> 4 columns at
@@ -331,28 +444,43 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
   }
 }
 
-template <typename T, int WAVES, int UB, bool VEC>
+template <typename T, int WAVES, int UB, bool VEC, bool CA, bool CB>
 hipError_t launch_one(const MatmulArgs& a, const SkinnyGeom& g, unsigned* counters, float* part) {
-  hipLaunchKernelGGL((skinny_kernel<T, WAVES, UB, VEC>), dim3((unsigned)g.nslabs, (unsigned)g.splits, (unsigned)g.nrb),
+  hipLaunchKernelGGL((skinny_kernel<T, WAVES, UB, VEC, CA, CB>), dim3((unsigned)g.nslabs, (unsigned)g.splits, (unsigned)g.nrb),
                      dim3(WAVES * 64), 0, a.stream, static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out,
                      (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo, (int)g.kc, counters, part);
   return hipGetLastError();
 }
 
+template <typename T, int WAVES, int UB, bool CA, bool CB>
+hipError_t launch_layout(const MatmulArgs& a, const SkinnyGeom& g, unsigned* counters, float* part) {
+  constexpr int CPL = Elem<T>::CPL, EPL = 16 / (int)sizeof(T);
+  auto aligned = [](const void* p, size_t n) { return reinterpret_cast<uintptr_t>(p) % n == 0; };
+  // Vector path: 16-byte loads of x2 that never straddle an edge (CPL
+  // columns of a row, or EPL k of a column), x1 loads of 4 (row-major x2) or
+  // EPL (column-major x2) consecutive k when x1 is row-major, float4 stores.
+  bool vec = a.ldo % 4 == 0 && aligned(a.out, 16) && aligned(a.x2, 16);
+  if constexpr (!CB)
+    vec = vec && a.N % CPL == 0 && a.ldx2 % CPL == 0 &&
+          (CA || (a.K % 4 == 0 && a.ldx1 % 4 == 0 && aligned(a.x1, 4 * sizeof(T))));
+  else
+    vec = vec && a.N % 4 == 0 && a.K % EPL == 0 && a.ldx2 % EPL == 0 &&
+          (CA || (a.ldx1 % EPL == 0 && aligned(a.x1, 16)));
+  return vec ? launch_one<T, WAVES, UB, true, CA, CB>(a, g, counters, part)
+             : launch_one<T, WAVES, UB, false, CA, CB>(a, g, counters, part);
+}
+
 template <typename T, int WAVES, int UB>
 hipError_t launch_skinny(const MatmulArgs& a) {
-  constexpr int CPL = Elem<T>::CPL;
   const SkinnyGeom g = skinny_geom(a.M, a.N, a.K, a.split_k, kSlabOf<T>);
-  // 16-byte row loads of x2 (CPL columns), 4 consecutive k of x1 per load,
-  // float4 stores of out.
-  const bool vec = (a.N % CPL == 0) && (a.ldx2 % CPL == 0) && (a.ldo % 4 == 0) && (a.K % 4 == 0) &&
-                   (a.ldx1 % 4 == 0) && (reinterpret_cast<uintptr_t>(a.x1) % (4 * sizeof(T)) == 0) &&
-                   (reinterpret_cast<uintptr_t>(a.x2) % 16 == 0) &&
-                   (reinterpret_cast<uintptr_t>(a.out) % 16 == 0);
   unsigned* counters = g.splits > 1 ? a.counters : nullptr;
   float* part = g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr;
-  return vec ? launch_one<T, WAVES, UB, true>(a, g, counters, part)
-             : launch_one<T, WAVES, UB, false>(a, g, counters, part);
+  switch (a.layout & 3) {
+    case 0: return launch_layout<T, WAVES, UB, false, false>(a, g, counters, part);
+    case TILEC_X1_COL_MAJOR: return launch_layout<T, WAVES, UB, true, false>(a, g, counters, part);
+    case TILEC_X2_COL_MAJOR: return launch_layout<T, WAVES, UB, false, true>(a, g, counters, part);
+    default: return launch_layout<T, WAVES, UB, true, true>(a, g, counters, part);
+  }
 }
 
 }  // namespace

@@ -60,16 +60,21 @@ int find(const char* name) {
 constexpr int64_t kMaxDim = (int64_t(1) << 31) - 1024;  // kernels index rows/cols in int32
 constexpr int kCUs = 256;                               // MI355X compute units
 
-// The skinny kernel addresses x2 within one 16-row block with 32-bit byte
-// offsets (row * ldx2 * 4, row < 16, must stay < 2^31), and its split-K
-// partials with 32-bit offsets (splits * row blocks * slabs * 16 * slab
-// width * 4 bytes < 2^31).  Row blocks of 16 are its grid's z dimension
-// (at most 65535).
+// The skinny kernel addresses its operands within one block with 32-bit byte
+// offsets: row-major x2 over 16 rows (16 * ldx2 * 4 bytes < 2^31), x1 over 16
+// rows or (column-major) up to 32 columns of K (32 * ldx1 * 2 bytes), and
+// column-major x2 over a slab's 64 fp32 / 128 bf16 columns (256 * ldx2
+// bytes < 2^31); its split-K partials also take 32-bit offsets (splits * row
+// blocks * slabs * 16 * slab width * 4 bytes < 2^31).  Row blocks of 16 are
+// its grid's z dimension (at most 65535).
 constexpr int64_t kSkinnyMaxLdx1 = int64_t(1) << 25;
 constexpr int64_t kSkinnyMaxLdx2 = int64_t(1) << 25;
+constexpr int64_t kSkinnyMaxLdx2ColMajor = int64_t(1) << 23;
 constexpr int64_t kSkinnyMaxRowBlocks = 65535;
 
-bool skinny_fits(int64_t ldx1, int64_t ldx2) { return ldx1 < kSkinnyMaxLdx1 && ldx2 < kSkinnyMaxLdx2; }
+bool skinny_fits(int64_t ldx1, int64_t ldx2, int layout) {
+  return ldx1 < kSkinnyMaxLdx1 && ldx2 < ((layout & TILEC_X2_COL_MAJOR) ? kSkinnyMaxLdx2ColMajor : kSkinnyMaxLdx2);
+}
 
 // Output tiles of the smallest tile GEMM (64 x 64): below kCUs of them the
 // tile GEMMs cannot fill the chip and the streaming kernel, which splits K,
@@ -93,10 +98,10 @@ size_t gemm_counter_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K,
 }
 
 // Built-in rule (used when the caller passes TILEC_VARIANT_AUTO).
-int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2) {
+int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2, int layout) {
   (void)K;
   if (dtype == TILEC_F32) {
-    if ((M <= 16 || small_output(M, N)) && cdiv(M, 16) <= kSkinnyMaxRowBlocks && skinny_fits(ldx1, ldx2))
+    if ((M <= 16 || small_output(M, N)) && cdiv(M, 16) <= kSkinnyMaxRowBlocks && skinny_fits(ldx1, ldx2, layout))
       return find("skinny_f32_w8_b1");
     static const char* order[] = {"gemm_f32_256x256x16_w2x2", "gemm_f32_256x128x16_w2x2",
                                   "gemm_f32_128x128x16_w2x2", "gemm_f32_128x64x16_w2x2"};
@@ -109,7 +114,7 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
   }
   // bf16: the streaming kernel for M <= 16 (it runs fp32 MFMAs on widened
   // inputs, so more rows are better served by the bf16 tile GEMMs).
-  if (M <= 16 && skinny_fits(ldx1, ldx2)) return find("skinny_bf16_w8_b1");
+  if (M <= 16 && skinny_fits(ldx1, ldx2, layout)) return find("skinny_bf16_w8_b1");
   static const char* order[] = {"gemm_bf16_256x256x64_r2", "gemm_bf16_256x128x64_r3", "gemm_bf16_128x128x64_r4"};
   for (const char* nm : order) {
     const int v = find(nm);
@@ -145,19 +150,24 @@ int auto_split(const VariantDesc* d, int64_t M, int64_t N, int64_t K) {
   return (int)s;
 }
 
-// ldx1 / ldx2 <= 0 mean "contiguous" (K and N).
+// ldx1 / ldx2 <= 0 mean "contiguous" (K and N for row-major operands, M and
+// K for column-major ones).
 int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int32_t split_k,
-            const VariantDesc** out_d, int* out_split, int64_t ldx1 = 0, int64_t ldx2 = 0) {
+            const VariantDesc** out_d, int* out_split, int64_t ldx1 = 0, int64_t ldx2 = 0, int layout = 0) {
   if (dtype != TILEC_F32 && dtype != TILEC_BF16)
     return fail(TILEC_ERR_TYPE, "tilec: unsupported dtype code %d (use float32 or bfloat16)", dtype);
   if (M < 0 || N < 0 || K < 0 || M > kMaxDim || N > kMaxDim || K > kMaxDim)
     return fail(TILEC_ERR_VALUE, "tilec: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
                 (long long)K);
   if (split_k < 0) return fail(TILEC_ERR_VALUE, "tilec: split_k must be >= 0 (got %d)", split_k);
+  if (layout & ~(TILEC_X1_COL_MAJOR | TILEC_X2_COL_MAJOR))
+    return fail(TILEC_ERR_VALUE, "tilec: unknown layout bits 0x%x", layout);
+  if (ldx1 <= 0) ldx1 = (layout & TILEC_X1_COL_MAJOR) ? M : K;
+  if (ldx2 <= 0) ldx2 = (layout & TILEC_X2_COL_MAJOR) ? K : N;
   const auto& t = table();
   int v = variant;
   if (v == TILEC_VARIANT_AUTO) {
-    v = auto_variant(M, N, K, dtype, ldx1 > 0 ? ldx1 : K, ldx2 > 0 ? ldx2 : N);
+    v = auto_variant(M, N, K, dtype, ldx1, ldx2, layout);
   } else if (v < 0 || v >= (int)t.size()) {
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: unknown variant %d (have %d)", v, (int)t.size());
   }
@@ -167,8 +177,9 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
   if (d->max_m > 0 && M > d->max_m)
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s takes M <= %d (got %lld)", d->name, d->max_m,
                 (long long)M);
-  if (d->family == TILEC_FAMILY_SKINNY && !skinny_fits(ldx1 > 0 ? ldx1 : K, ldx2 > 0 ? ldx2 : N))
-    return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s needs ldx1 < 2^25 and ldx2 < 2^25", d->name);
+  if (d->family == TILEC_FAMILY_SKINNY && !skinny_fits(ldx1, ldx2, layout))
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s needs ldx1 < 2^25 and ldx2 < 2^%d", d->name,
+                (layout & TILEC_X2_COL_MAJOR) ? 23 : 25);
   int s = split_k == 0 ? auto_split(d, M, N, K) : split_k;
   if (d->family == TILEC_FAMILY_GEMM) {
     const SplitGeom g = gemm_split_geom(K, d->bk, s);
@@ -202,20 +213,24 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
 extern "C" {
 
 int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t N, int64_t K, int64_t ldx1,
-                 int64_t ldx2, int64_t ldo, int32_t dtype, int32_t variant, int32_t split_k, void* workspace,
-                 size_t workspace_bytes, void* counters, size_t counter_bytes, void* stream) {
+                 int64_t ldx2, int64_t ldo, int32_t layout, int32_t dtype, int32_t variant, int32_t split_k,
+                 void* workspace, size_t workspace_bytes, void* counters, size_t counter_bytes, void* stream) {
   g_err[0] = 0;
   const VariantDesc* d = nullptr;
   int s = 1;
-  int rc = resolve(M, N, K, dtype, variant, split_k, &d, &s, ldx1, ldx2);
+  int rc = resolve(M, N, K, dtype, variant, split_k, &d, &s, ldx1, ldx2, layout);
   if (rc != TILEC_OK) return rc;
   if (M == 0 || N == 0) return TILEC_OK;
   if (ldo < N) return fail(TILEC_ERR_VALUE, "tilec: ldo=%lld < N=%lld", (long long)ldo, (long long)N);
   if (out == nullptr) return fail(TILEC_ERR_VALUE, "tilec: out is NULL");
   if (K > 0) {
     if (x1 == nullptr || x2 == nullptr) return fail(TILEC_ERR_VALUE, "tilec: x1/x2 is NULL");
-    if (ldx1 < K) return fail(TILEC_ERR_VALUE, "tilec: ldx1=%lld < K=%lld", (long long)ldx1, (long long)K);
-    if (ldx2 < N) return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < N=%lld", (long long)ldx2, (long long)N);
+    const bool c1 = layout & TILEC_X1_COL_MAJOR, c2 = layout & TILEC_X2_COL_MAJOR;
+    const int64_t need1 = c1 ? M : K, need2 = c2 ? K : N;
+    if (ldx1 < need1)
+      return fail(TILEC_ERR_VALUE, "tilec: ldx1=%lld < %s=%lld", (long long)ldx1, c1 ? "M" : "K", (long long)need1);
+    if (ldx2 < need2)
+      return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < %s=%lld", (long long)ldx2, c2 ? "K" : "N", (long long)need2);
   }
   const bool skinny = d->family == TILEC_FAMILY_SKINNY;
   const size_t need = skinny ? skinny_workspace_bytes(dtype, M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
@@ -236,6 +251,7 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
   a.ldx1 = ldx1 > 0 ? ldx1 : 1;
   a.ldx2 = ldx2 > 0 ? ldx2 : 1;
   a.ldo = ldo;
+  a.layout = layout;
   a.split_k = s;
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
@@ -271,7 +287,7 @@ int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {
   int s = 1;
   const int rc = resolve(M, N, K, dtype, TILEC_VARIANT_AUTO, 0, &d, &s);
   if (rc != TILEC_OK) return -rc;
-  return auto_variant(M, N, K, dtype, K, N);
+  return auto_variant(M, N, K, dtype, K, N, 0);
 }
 
 int32_t tilec_auto_split_k(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant) {
@@ -305,6 +321,6 @@ int tilec_variant_info(int32_t variant, int32_t info[8], const char** name) {
 
 const char* tilec_last_error(void) { return g_err; }
 
-int32_t tilec_version(void) { return 10000; }
+int32_t tilec_version(void) { return 10100; }
 
 }  // extern "C"

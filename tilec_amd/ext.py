@@ -202,17 +202,29 @@ def counters_for(device, stream, nbytes):
 # ---------------------------------------------------------------------------
 
 def _operand(x, rows, cols):
-    """(tensor, row stride) usable by the kernels: unit column stride and a
-    row stride >= cols; otherwise the reference's `.contiguous()` copy
-    (tilec/ext.py:59-60)."""
-    if rows <= 1 or cols == 0:
-        if not x.is_contiguous():
-            x = x.contiguous()
-        return x, max(cols, 1)
-    if x.stride(1) == 1 and x.stride(0) >= cols:
-        return x, x.stride(0)
-    x = x.contiguous()
-    return x, max(cols, 1)
+    """(tensor, leading dimension, column-major?) the kernels read in place:
+    row-major with unit column stride and a row stride >= cols, or
+    column-major (the transposed view x.T of a row-major matrix) with unit
+    row stride and a column stride >= rows; anything else (broadcast,
+    negative or doubly strided views) gets the reference's `.contiguous()`
+    copy (tilec/ext.py:59-60).  Size-1 dimensions impose no stride."""
+    if rows == 0 or cols == 0:
+        return x, max(cols, 1), False
+    s0, s1 = x.stride()
+    if (cols == 1 or s1 == 1) and (rows == 1 or s0 >= cols):
+        return x, (s0 if rows > 1 else cols), False
+    if (rows == 1 or s0 == 1) and (cols == 1 or s1 >= rows):
+        return x, (s1 if cols > 1 else rows), True
+    return x.contiguous(), cols, False
+
+
+def layout_of(x1, x2):
+    """The layout bits tilec_matmul gets for these operands (0 = both
+    row-major; after a `.contiguous()` copy an operand is row-major)."""
+    M, K = x1.shape
+    N = x2.shape[1]
+    return ((_lib.X1_COL_MAJOR if _operand(x1, M, K)[2] else 0) |
+            (_lib.X2_COL_MAJOR if _operand(x2, K, N)[2] else 0))
 
 
 def _prepare(x1, x2):
@@ -234,8 +246,9 @@ def _prepare(x1, x2):
 
 def _launch(x1, x2, M, K, N, variant, split_k):
     dtype = _lib.F32 if x1.dtype == torch.float32 else _lib.BF16
-    a, lda = _operand(x1, M, K)
-    b, ldb = _operand(x2, K, N)
+    a, lda, ca = _operand(x1, M, K)
+    b, ldb, cb = _operand(x2, K, N)
+    layout = (_lib.X1_COL_MAJOR if ca else 0) | (_lib.X2_COL_MAJOR if cb else 0)
     out = torch.empty((M, N), dtype=torch.float32, device=x1.device)
     if M == 0 or N == 0:
         return out
@@ -248,7 +261,7 @@ def _launch(x1, x2, M, K, N, variant, split_k):
         ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
         cnt = counters_for(x1.device, stream, L.tilec_matmul_counter_bytes(M, N, K, dtype, variant, split_k))
         cnt_ptr, cnt_bytes = cnt.data_ptr(), cnt.numel()
-    _lib.check(L.tilec_matmul(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, lda, ldb, N,
+    _lib.check(L.tilec_matmul(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, lda, ldb, N, layout,
                               dtype, variant, split_k, ws_ptr, ws_bytes, cnt_ptr, cnt_bytes, stream))
     return out
 
@@ -272,8 +285,10 @@ def matrix_mul(x1, x2, config=None):
     """out[M,N] (float32) = x1[M,K] · x2[K,N] on the GPU.
 
     Same contract as the reference (tilec/ext.py:54-67): ValueError when K does
-    not match, strided inputs are made contiguous, the output is new.  Inputs
-    are float32, or bfloat16 (fp32 accumulate, fp32 output).  `config`
+    not match, the output is new.  Inputs are float32, or bfloat16 (fp32
+    accumulate, fp32 output).  Row-strided and transposed views (x.T) are
+    read in place; only other strided views get the reference's
+    `.contiguous()` copy.  `config`
     (optional, as the reference's tuner passes it, tilec/tune.py:37) forces a
     (variant, split_k) from `hip_configs`.
     """
