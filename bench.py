@@ -9,12 +9,16 @@ are timed between HIP events on the stream the kernel runs on, after W
 warmup steps.  Extra objects in the same line:
   roofline     — the 4096^3 kernel against the fp32 MFMA peak (157.3 TFLOP/s)
   skinny       — the metric's "GB/s + %HBM roofline at M<=16" (config 1):
-                 M in {1,4,16}, K=N=4096, x2 rotated over 8 buffers (512 MiB,
-                 beyond the 256 MB Infinity Cache), launches replayed from a
-                 HIP graph so the host does not bound an 8 us kernel
+                 M in {1,4,16} fp32 and {1,16} bf16, K=N=4096, x2 rotated
+                 over 512 MiB of copies (beyond the 256 MB Infinity Cache),
+                 launches replayed from a HIP graph so the host does not
+                 bound an 8 us kernel
   bf16_8192    — config 4, bf16 8192^3 with fp32 accumulate, vs 2.5 PFLOP/s
   configs      — every fp32 config (0, 2 at 1024/2048/4096, the 4 ragged
                  shapes of 3): device time per call from graph replay
+  layouts      — transposed operands read in place: x @ W.T GEMV (weight
+                 W [N, K] row-major) as in `skinny`, and the 4096^3 fp32 /
+                 8192^3 bf16 GEMMs with x1, x2 or both column-major
   cpu_baseline — the oracle's tiled C restatement of the reference kernel
                  (oracle/matmul_oracle.c, OpenMP) on a bounded row sample of
                  the same 4096^3 problem, on this box's host cores; plus
@@ -43,7 +47,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the skinny and bf16 sections")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
-    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "copy"],
+    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "copy"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -95,46 +99,90 @@ def bench_square(args):
     return dict(ms=ms, tflops=tflops, config=cfg)
 
 
-def bench_skinny(steps=200):
-    """M in {1,4,16} fp32 and {1,16} bf16 at K=N=4096: HBM GB/s from graph-replayed
-    launches over rotating x2 copies (>= 512 MB per dtype, so neither L2 nor the
-    256 MB MALL serves a repeat)."""
+def _gemv(x1, x2s, steps):
+    """us per launch of x1 @ x2s[i] over rotating x2 buffers, launches
+    replayed from a HIP graph (an ~8 us kernel is not host-bound)."""
+    import torch
+    from tilec_amd import ext
+    nbuf = len(x2s)
+    for i in range(nbuf):  # warm up: workspace exists before capture
+        ext.matrix_mul(x1, x2s[i])
+    torch.cuda.synchronize()
+    reps = 4 * nbuf
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ext.matrix_mul(x1, x2s[0])
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            outs = [ext.matrix_mul(x1, x2s[i % nbuf]) for i in range(reps)]
+    torch.cuda.synchronize()
+    replays = max(1, steps // reps)
+    with torch.cuda.stream(s):
+        ms = timed(g.replay, replays, 2, stream=s) / reps
+    del outs
+    return ms * 1e3
+
+
+def _gemv_cases(ms_by_dtype, transposed, steps):
+    """M x 4096 @ 4096 x 4096 per (dtype, M): x2 row-major, or (transposed)
+    the column-major view W.T of a row-major weight W [N, K].  Rotating x2
+    copies total >= 512 MB per dtype, so neither L2 nor the 256 MB MALL
+    serves a repeat."""
     import torch
     from oracle import oracle as O
     from tilec_amd import ext
     K = N = 4096
     out = {}
-    for dtype, Ms in (("f32", (1, 4, 16)), ("bf16", (1, 16))):
+    for dtype, Ms in ms_by_dtype:
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         esz = 4 if dtype == "f32" else 2
         nbuf = (512 << 20) // (esz * K * N)
         x2s = [torch.from_numpy(O.normal((K, N), 3 + 1000 * i)).to(tdt).cuda() for i in range(nbuf)]
+        if transposed:  # the same values, stored as W [N, K] and passed as W.T
+            x2s = [x.t().contiguous().t() for x in x2s]
         for M in Ms:
             x1 = torch.from_numpy(O.normal((M, K), 2)).to(tdt).cuda()
+            assert ext.layout_of(x1, x2s[0]) == (2 if transposed else 0)
             cfg = kernel_name_for(M, K, N, dtype)
-            for i in range(nbuf):  # warm up: workspace exists before capture
-                ext.matrix_mul(x1, x2s[i])
-            torch.cuda.synchronize()
-            reps = 4 * nbuf
-            g = torch.cuda.CUDAGraph()
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(s):
-                ext.matrix_mul(x1, x2s[0])
-                torch.cuda.synchronize()
-                with torch.cuda.graph(g, stream=s):
-                    outs = [ext.matrix_mul(x1, x2s[i % nbuf]) for i in range(reps)]
-            torch.cuda.synchronize()
-            replays = max(1, steps // reps)
-            with torch.cuda.stream(s):
-                ms = timed(g.replay, replays, 2, stream=s) / reps
-            del outs
+            us = _gemv(x1, x2s, steps)
             nbytes = esz * (M * K + K * N) + 4 * M * N
-            gbs = nbytes / (ms * 1e-3) / 1e9
-            key = f"M{M}" if dtype == "f32" else f"bf16_M{M}"
-            out[key] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, config=list(cfg))
-            log(f"skinny {dtype} M={M}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({cfg})")
+            gbs = nbytes / (us * 1e-6) / 1e9
+            key = (f"M{M}" if dtype == "f32" else f"bf16_M{M}")
+            out[key] = dict(us=us, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, config=list(cfg))
+            log(f"gemv {dtype} M={M}{' x @ W.T' if transposed else ''}: {us:.2f} us/launch, {gbs:.0f} GB/s ({cfg})")
         del x2s
+    return out
+
+
+def bench_skinny(steps=200):
+    """M in {1,4,16} fp32 and {1,16} bf16 at K=N=4096: HBM GB/s from
+    graph-replayed launches over rotating x2 copies."""
+    return _gemv_cases((("f32", (1, 4, 16)), ("bf16", (1, 16))), False, steps)
+
+
+def bench_layouts(steps=200, gemm_steps=20):
+    """Transposed operands read in place (no .contiguous() copy): x @ W.T
+    GEMV (x2 column-major) as in the skinny section, and the fp32 4096^3 and
+    bf16 8192^3 GEMMs with x1, x2 or both column-major."""
+    import torch
+    from oracle import oracle as O
+    from tilec_amd import ext
+    out = {"gemv_x_WT": _gemv_cases((("f32", (1, 16)), ("bf16", (1, 16))), True, steps)}
+    for dtype, n, peak in (("f32", 4096, PEAK_FP32_MFMA), ("bf16", 8192, PEAK_BF16_MFMA)):
+        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+        a = torch.from_numpy(O.uniform((n, n), 4)).to(tdt).cuda()
+        b = torch.from_numpy(O.uniform((n, n), 5)).to(tdt).cuda()
+        at, bt = a.t().contiguous().t(), b.t().contiguous().t()  # same values, column-major
+        cfg = kernel_name_for(n, n, n, dtype)
+        for name, x1, x2 in (("x1T", at, b), ("x2T", a, bt), ("x1T_x2T", at, bt)):
+            ms = timed(lambda: ext.matrix_mul(x1, x2), gemm_steps, 3)
+            tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
+            out[f"{dtype}_{n}_{name}"] = dict(ms=ms, TFLOPs=tflops, frac=tflops / peak, layout=ext.layout_of(x1, x2),
+                                              config=list(cfg))
+            log(f"{dtype} {n}^3 {name}: {ms:.3f} ms, {tflops:.1f} TFLOP/s ({cfg})")
+        del a, b, at, bt
     return out
 
 
@@ -287,7 +335,7 @@ def main():
 
     if args.only:
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
-               "configs": bench_configs, "copy": bench_copy}[args.only]()
+               "configs": bench_configs, "layouts": bench_layouts, "copy": bench_copy}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return
 
@@ -297,6 +345,7 @@ def main():
         extra["skinny"] = bench_skinny()
         extra["bf16_8192"] = bench_bf16()
         extra["configs"] = bench_configs()
+        extra["layouts"] = bench_layouts()
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
 
     rec = {
