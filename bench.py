@@ -74,9 +74,9 @@ def timed(fn, steps, warmup, stream=None):
     return s.elapsed_time(e) / steps
 
 
-def kernel_name_for(M, K, N, dtype):
+def kernel_name_for(M, K, N, dtype, layout=0):
     from tilec_amd import _lib, tune
-    p = tune.pick(M, K, N, dtype)
+    p = tune.pick(M, K, N, dtype, layout)
     if p is not None:
         return p
     L = _lib.lib()
@@ -145,7 +145,7 @@ def _gemv_cases(ms_by_dtype, transposed, steps):
         for M in Ms:
             x1 = torch.from_numpy(O.normal((M, K), 2)).to(tdt).cuda()
             assert ext.layout_of(x1, x2s[0]) == (2 if transposed else 0)
-            cfg = kernel_name_for(M, K, N, dtype)
+            cfg = kernel_name_for(M, K, N, dtype, 2 if transposed else 0)
             us = _gemv(x1, x2s, steps)
             nbytes = esz * (M * K + K * N) + 4 * M * N
             gbs = nbytes / (us * 1e-6) / 1e9
@@ -175,8 +175,8 @@ def bench_layouts(steps=200, gemm_steps=20):
         a = torch.from_numpy(O.uniform((n, n), 4)).to(tdt).cuda()
         b = torch.from_numpy(O.uniform((n, n), 5)).to(tdt).cuda()
         at, bt = a.t().contiguous().t(), b.t().contiguous().t()  # same values, column-major
-        cfg = kernel_name_for(n, n, n, dtype)
         for name, x1, x2 in (("x1T", at, b), ("x2T", a, bt), ("x1T_x2T", at, bt)):
+            cfg = kernel_name_for(n, n, n, dtype, ext.layout_of(x1, x2))
             ms = timed(lambda: ext.matrix_mul(x1, x2), gemm_steps, 3)
             tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
             out[f"{dtype}_{n}_{name}"] = dict(ms=ms, TFLOPs=tflops, frac=tflops / peak, layout=ext.layout_of(x1, x2),

@@ -126,11 +126,18 @@ def test_gemm_split_geometry_matches_the_library():
 
 def test_tune_features_and_shapes():
     f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8)
-    assert len(f) == 16 and all(math.isfinite(x) for x in f)
-    s = tune.shapes(120, seed=0)
-    assert len(s) == 120 + len(tune.CONFIG_SHAPES) and s == tune.shapes(120, seed=0)
-    assert set(tune.CONFIG_SHAPES) <= set(s)
-    assert any(m <= 16 for m, _, _, _ in s) and any(d == "bf16" for *_, d in s)
+    assert len(f) == 18 and all(math.isfinite(x) for x in f) and f[-2:] == [0.0, 0.0]
+    assert tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8, layout=3)[-2:] == [1.0, 1.0]
+    s = tune.shapes(120, seed=0, n_layout=40)
+    assert s == tune.shapes(120, seed=0, n_layout=40)
+    rm = [x for x in s if x[4] == 0]
+    lay = [x for x in s if x[4] != 0]
+    assert len(rm) == 120 + len(tune.CONFIG_SHAPES) and len(lay) == 40 + len(tune.LAYOUT_CONFIG_SHAPES)
+    assert {x + (0,) for x in tune.CONFIG_SHAPES} <= set(rm) and set(tune.LAYOUT_CONFIG_SHAPES) <= set(lay)
+    assert {x[4] for x in lay} == {1, 2, 3}
+    assert any(m <= 16 for m, *_ in s) and any(d == "bf16" for _, _, _, d, _ in s)
+    # the row-major draws do not depend on the layout stream
+    assert rm == [x for x in tune.shapes(120, seed=0, n_layout=5) if x[4] == 0]
 
 
 def test_tune_rotating_operands():
@@ -175,9 +182,11 @@ def test_pick_uses_measured_best_for_benchmarked_shapes():
     if not os.path.exists(tune.DATA) or not os.path.exists(tune.MODEL):
         pytest.skip("no MI355X tuning data committed yet")
     best = tune.best_table(tune.load())
-    for shape in tune.CONFIG_SHAPES:
-        want = tuple(best[",".join(map(str, shape))])
-        assert tune.pick(*shape) == want, shape
+    for shape in [s + (0,) for s in tune.CONFIG_SHAPES] + tune.LAYOUT_CONFIG_SHAPES:
+        key = ",".join(map(str, shape))
+        if key not in best:
+            continue  # not benchmarked in this layout yet
+        assert tune.pick(*shape) == tuple(best[key]), shape
 
 
 def test_committed_tuning_data_schema():

@@ -266,11 +266,12 @@ def _launch(x1, x2, M, K, N, variant, split_k):
     return out
 
 
-def _resolve_config(config, M, K, N, dtype):
-    """config: None (tuned pick), a variant name / id, or (variant, split_k)."""
+def _resolve_config(config, M, K, N, dtype, layout=0):
+    """config: None (tuned pick for this shape and layout), a variant name /
+    id, or (variant, split_k)."""
     if config is None:
         from . import tune
-        config = tune.pick(M, K, N, "bf16" if dtype == torch.bfloat16 else "f32")
+        config = tune.pick(M, K, N, "bf16" if dtype == torch.bfloat16 else "f32", layout)
         if config is None:
             return _lib.VARIANT_AUTO, 0
     if isinstance(config, (str, int)):
@@ -293,7 +294,7 @@ def matrix_mul(x1, x2, config=None):
     (variant, split_k) from `hip_configs`.
     """
     M, K, N = _prepare(x1, x2)
-    variant, split_k = _resolve_config(config, M, K, N, x1.dtype)
+    variant, split_k = _resolve_config(config, M, K, N, x1.dtype, layout_of(x1, x2) if config is None else 0)
     return _launch(x1, x2, M, K, N, variant, split_k)
 
 

@@ -35,7 +35,7 @@ from .language import cdiv
 HERE = os.path.dirname(os.path.abspath(__file__))
 DATA = os.path.join(HERE, "mm_bench_mi355x.csv")
 MODEL = os.path.join(HERE, "mm_model_mi355x.json")
-FIELDS = ["chip", "cus", "M", "K", "N", "dtype", "kernel", "BM", "BN", "BK", "split_k", "ms"]
+FIELDS = ["chip", "cus", "M", "K", "N", "dtype", "layout", "kernel", "BM", "BN", "BK", "split_k", "ms"]
 
 
 @lru_cache(None)
@@ -53,11 +53,12 @@ def _variant_by_name():
     return {v["name"]: v for v in _lib.variants()}
 
 
-def features(M, K, N, cus, dtype, kernel, split_k):
+def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
     """Model inputs for one (shape, config); the role of tilec/tune.py:29-32.
 
     Shape and config sizes enter as log2, plus the derived quantities that
-    decide occupancy: workgroups launched per CU and the K rows per split.
+    decide occupancy: workgroups launched per CU and the K rows per split,
+    and the operand layout bits (x1, x2 column-major).
     """
     v = _variant_by_name()[kernel]
     tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
@@ -66,7 +67,8 @@ def features(M, K, N, cus, dtype, kernel, split_k):
     return [lg(M), lg(K), lg(N), cus, 1.0 if dtype == "bf16" else 0.0,
             float(v["family"]), lg(v["bm"]), lg(v["bn"]), lg(v["bk"]), float(v["waves"]),
             float(v["unroll"]), lg(split_k), lg(tiles), math.log2(max(1, wgs) / cus),
-            lg(cdiv(K, split_k)), lg(M * K * N)]
+            lg(cdiv(K, split_k)), lg(M * K * N),
+            float(layout & _lib.X1_COL_MAJOR != 0), float(layout & _lib.X2_COL_MAJOR != 0)]
 
 
 GRAPH_BELOW_MS = 0.2   # calls shorter than this are timed from a replayed HIP graph
@@ -141,7 +143,7 @@ def time_ms(x1, x2, config, best=None, reps=5, x2s=None):
     return sorted(times)[reps // 2]
 
 
-# The BASELINE.json configurations, always part of the tuning set.
+# The BASELINE.json configurations, always part of the tuning set (row-major).
 CONFIG_SHAPES = [
     (512, 4096, 64, "f32"),
     (1, 4096, 4096, "f32"), (4, 4096, 4096, "f32"), (16, 4096, 4096, "f32"),
@@ -150,42 +152,83 @@ CONFIG_SHAPES = [
     (8192, 8192, 8192, "bf16"), (4096, 4096, 4096, "bf16"),
     (1, 4096, 4096, "bf16"), (16, 4096, 4096, "bf16"),
 ]
+# The same sizes with transposed operands (x @ W.T GEMV, TN / NT / TT GEMMs).
+LAYOUT_CONFIG_SHAPES = [
+    (1, 4096, 4096, "f32", 2), (4, 4096, 4096, "f32", 2), (16, 4096, 4096, "f32", 2),
+    (1, 4096, 4096, "bf16", 2), (16, 4096, 4096, "bf16", 2),
+    (4096, 4096, 4096, "f32", 1), (4096, 4096, 4096, "f32", 2), (4096, 4096, 4096, "f32", 3),
+    (8192, 8192, 8192, "bf16", 1), (8192, 8192, 8192, "bf16", 2), (8192, 8192, 8192, "bf16", 3),
+]
 
 
-def shapes(n=500, seed=0):
-    """Seeded random shapes (M, K, N, dtype), plus CONFIG_SHAPES.
+def _draw(rng):
+    """One shape of the reference's log-uniform generator with its size
+    limits (tilec/tune.py:54-65; there x1 is [M1,N] and x2 is [N,M2], so its
+    N is our K), widened to the regimes MI355X serves differently: skinny M
+    in [1, 16] (fp32 and bf16), bf16 tile GEMMs and ragged sizes.  None when
+    the draw breaks a size limit."""
+    kind = rng.random()
+    M = round(2 ** rng.uniform(7, 13))
+    K = round(2 ** rng.uniform(8, 14))
+    N = round(2 ** rng.uniform(5, 12))
+    dtype = "f32"
+    if rng.random() < 0.5:
+        K = 1 << round(math.log2(K))
+    if kind < 0.3:                      # skinny (a third of them bf16)
+        M = rng.randint(1, 16)
+        N = round(2 ** rng.uniform(8, 14))
+        if kind < 0.1:
+            dtype = "bf16"
+    elif kind < 0.55:                   # bf16 tile GEMM
+        dtype = "bf16"
+    if M * K * N <= 1 << 33 and M * K <= 1 << 26 and K * N <= 1 << 26:
+        return M, K, N, dtype
+    return None
 
-    Keeps the reference's log-uniform generator with its size limits
-    (tilec/tune.py:54-65; there x1 is [M1,N] and x2 is [N,M2], so its N is
-    our K) and adds the regimes MI355X serves differently: skinny M in
-    [1, 16] (fp32 and bf16), bf16 tile GEMMs, and ragged sizes.
-    """
+
+def shapes(n=500, seed=0, n_layout=120):
+    """Seeded random shapes (M, K, N, dtype, layout): `n` row-major draws plus
+    CONFIG_SHAPES, and `n_layout` draws of a second stream (seed + 1) with a
+    random non-row-major layout, plus LAYOUT_CONFIG_SHAPES."""
     rng = random.Random(seed)
     out = set(CONFIG_SHAPES)
     while len(out) < n + len(CONFIG_SHAPES):
-        kind = rng.random()
-        M = round(2 ** rng.uniform(7, 13))
-        K = round(2 ** rng.uniform(8, 14))
-        N = round(2 ** rng.uniform(5, 12))
-        dtype = "f32"
-        if rng.random() < 0.5:
-            K = 1 << round(math.log2(K))
-        if kind < 0.3:                      # skinny (a third of them bf16)
-            M = rng.randint(1, 16)
-            N = round(2 ** rng.uniform(8, 14))
-            if kind < 0.1:
-                dtype = "bf16"
-        elif kind < 0.55:                   # bf16 tile GEMM
-            dtype = "bf16"
-        if M * K * N <= 1 << 33 and M * K <= 1 << 26 and K * N <= 1 << 26:
-            out.add((M, K, N, dtype))
-    return sorted(out, key=lambda s: s[0] * s[1] * s[2])
+        d = _draw(rng)
+        if d is not None:
+            out.add(d)
+    out = {s + (0,) for s in out}
+    rng2 = random.Random(seed + 1)
+    lay = set(LAYOUT_CONFIG_SHAPES)
+    while len(lay) < n_layout + len(LAYOUT_CONFIG_SHAPES):
+        d = _draw(rng2)
+        if d is not None:
+            lay.add(d + (rng2.choice((1, 2, 2, 3)),))  # x @ W.T (x2 column-major) twice as often
+    return sorted(out | lay, key=lambda s: (s[0] * s[1] * s[2], s))
+
+
+def operands(M, K, N, dtype, layout, gen):
+    """Random N(0,1) operands of a shape, laid out as asked (a column-major
+    operand is the transposed view of a row-major buffer)."""
+    import torch
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    x1 = torch.randn(M, K, generator=gen, device="cuda").to(tdt)
+    x2 = torch.randn(K, N, generator=gen, device="cuda").to(tdt)
+    if layout & _lib.X1_COL_MAJOR:
+        x1 = x1.t().contiguous().t()
+    if layout & _lib.X2_COL_MAJOR:
+        x2 = x2.t().contiguous().t()
+    return x1, x2
 
 
 def load(path=None):
+    """Rows of a timing CSV; files written before the layout column count as
+    row-major."""
     with open(path or DATA) as f:
-        return [{k: (v if k in ("chip", "dtype", "kernel") else float(v)) for k, v in r.items()}
+        rows = [{k: (v if k in ("chip", "dtype", "kernel") else float(v)) for k, v in r.items()}
                 for r in csv.DictReader(f)]
+    for r in rows:
+        r["layout"] = int(r.get("layout", 0) or 0)
+    return rows
 
 
 def bench(n=300, seed=0, path=None):
@@ -196,37 +239,39 @@ def bench(n=300, seed=0, path=None):
     from . import ext
     path = path or DATA
     chip, cus = machine()
-    done = {(int(r["M"]), int(r["K"]), int(r["N"]), r["dtype"]) for r in load(path)} if os.path.exists(path) else set()
+    done = {_key(r) for r in load(path)} if os.path.exists(path) else set()
     with open(path, "a", newline="") as f:
         w = csv.writer(f)
         if not done:
             w.writerow(FIELDS)
         g = torch.Generator(device="cuda").manual_seed(seed)
         todo = shapes(n, seed)
-        for i, (M, K, N, dtype) in enumerate(todo):
-            if (M, K, N, dtype) in done:
+        for i, (M, K, N, dtype, layout) in enumerate(todo):
+            if (M, K, N, dtype, layout) in done:
                 continue
-            tdt = torch.float32 if dtype == "f32" else torch.bfloat16
-            x1 = torch.randn(M, K, generator=g, device="cuda").to(tdt)
-            x2 = torch.randn(K, N, generator=g, device="cuda").to(tdt)
+            x1, x2 = operands(M, K, N, dtype, layout, g)
             best = None
             x2s = operands_for(M, K, N, x2)
+            if layout & _lib.X2_COL_MAJOR:  # keep the copies column-major
+                x2s = [x2] + [x.t().contiguous().t() for x in x2s[1:]]
             for kernel, split in ext.hip_configs(M, K, N, dtype):
                 v = _variant_by_name()[kernel]
                 ms = time_ms(x1, x2, (kernel, split), best, x2s=x2s)
                 best = ms if best is None else min(best, ms)
-                w.writerow([chip, cus, M, K, N, dtype, kernel, v["bm"], v["bn"], v["bk"], split, f"{ms:.6g}"])
+                w.writerow([chip, cus, M, K, N, dtype, layout, kernel, v["bm"], v["bn"], v["bk"], split,
+                            f"{ms:.6g}"])
             f.flush()
             del x2s
-            print(f"{i + 1}/{len(todo)}  {M}x{K} @ {K}x{N} {dtype}  best {best:.4f} ms", flush=True)
+            print(f"{i + 1}/{len(todo)}  {M}x{K} @ {K}x{N} {dtype} layout {layout}  best {best:.4f} ms", flush=True)
 
 
 def row_features(r):
-    return features(int(r["M"]), int(r["K"]), int(r["N"]), r["cus"], r["dtype"], r["kernel"], int(r["split_k"]))
+    return features(int(r["M"]), int(r["K"]), int(r["N"]), r["cus"], r["dtype"], r["kernel"], int(r["split_k"]),
+                    int(r["layout"]))
 
 
 def _key(r):
-    return (int(r["M"]), int(r["K"]), int(r["N"]), r["dtype"])
+    return (int(r["M"]), int(r["K"]), int(r["N"]), r["dtype"], int(r["layout"]))
 
 
 def train(test_frac=0.2, seed=0, out=MODEL, path=None):
@@ -258,7 +303,7 @@ def train(test_frac=0.2, seed=0, out=MODEL, path=None):
         best = min(r["ms"] for r in rs)
         pred = model.predict([row_features(r) for r in rs])
         chosen = rs[min(range(len(rs)), key=lambda i: pred[i])]
-        M, K, N, dtype = k
+        M, K, N, dtype, _ = k
         dcode = _lib.F32 if dtype == "f32" else _lib.BF16
         auto = _lib.variants()[L.tilec_select_variant(M, N, K, dcode)]["name"]
         auto_split = L.tilec_auto_split_k(M, N, K, dcode, _lib.variant_id(auto))
@@ -283,7 +328,7 @@ def train(test_frac=0.2, seed=0, out=MODEL, path=None):
 
 
 def best_table(rows):
-    """Measured argmin per benchmarked shape: {"M,K,N,dtype": [kernel, split_k]}."""
+    """Measured argmin per benchmarked shape: {"M,K,N,dtype,layout": [kernel, split_k]}."""
     best = {}
     for r in rows:
         k = _key(r)
@@ -322,8 +367,10 @@ class TreeModel:
         self.n_features = data["n_features"]
         self.trees = [{k: np.asarray(t[k]) for k in ("left", "right", "feature", "threshold", "value")}
                       for t in data["trees"]]
-        self.best = {tuple(int(x) if i < 3 else x for i, x in enumerate(k.split(","))): tuple(v)
-                     for k, v in data.get("best", {}).items()}
+        self.best = {}
+        for k, v in data.get("best", {}).items():
+            f = k.split(",")
+            self.best[(int(f[0]), int(f[1]), int(f[2]), f[3], int(f[4]) if len(f) > 4 else 0)] = tuple(v)
 
     def predict(self, X):
         import numpy as np
@@ -353,10 +400,11 @@ def _model(path=MODEL):
 
 
 @lru_cache(4096)
-def pick(M, K, N, dtype="f32"):
+def pick(M, K, N, dtype="f32", layout=0):
     """(variant name, split_k) with the least predicted time, or None to use
     the library's built-in rule (tilec/tune.py:143-151).  A shape that was
-    benchmarked exactly takes its measured best config (when still offered)."""
+    benchmarked exactly (in this layout) takes its measured best config
+    (when still offered)."""
     model = _model()
     if model is None or 0 in (M, K, N):
         return None
@@ -364,11 +412,13 @@ def pick(M, K, N, dtype="f32"):
     cands = ext.hip_configs(M, K, N, dtype)
     if not cands:
         return None
-    measured = model.best.get((M, K, N, dtype))
+    measured = model.best.get((M, K, N, dtype, layout))
     if measured is not None and measured in cands:
         return measured
     cus = _cus()
-    pred = model.predict([features(M, K, N, cus, dtype, k, s) for k, s in cands])
+    if model.n_features < len(features(M, K, N, cus, dtype, cands[0][0], cands[0][1], layout)):
+        return None  # a model from before the layout features: use the built-in rule
+    pred = model.predict([features(M, K, N, cus, dtype, k, s, layout) for k, s in cands])
     return cands[int(pred.argmin())]
 
 
