@@ -141,6 +141,32 @@ int32_t tilec_auto_split_k(int64_t M, int64_t N, int64_t K, int32_t dtype,
 int32_t tilec_num_variants(void);
 int tilec_variant_info(int32_t variant, int32_t info[8], const char** name);
 
+/*
+ * Row or column sums of a matrix, fp32 accumulate, fp32 out:
+ *   axis 1:  out[r] = sum_c x[r][c]   (R outputs)
+ *   axis 0:  out[c] = sum_r x[r][c]   (C outputs)
+ * x is R x C, float32 or bfloat16, row-major with row stride ldx (>= C), or
+ * column-major when `layout` is TILEC_X1_COL_MAJOR (column stride ldx >= R).
+ * A sum over zero elements is 0.
+ *
+ * The reduction the reference plans as `tl.sum` (README.md:88) and shows as
+ * the `row_sum` kernel (kernel1.py:8-15: out[r] = tl.sum(x[r, :]); the
+ * op-level spelling `tl.ext.sum(x_ptr, axis=1)` at kernel1.py:15).  Long
+ * reductions with few outputs are split across workgroups and combined in
+ * a fixed order, so results do not depend on scheduling; they need the
+ * `workspace` and zeroed `counters` that tilec_sum_workspace_bytes /
+ * tilec_sum_counter_bytes give (0 when not split), under the same rules as
+ * tilec_matmul's (counters are left zero; concurrent calls need their own).
+ */
+int tilec_sum(const void* x, float* out, int64_t R, int64_t C, int64_t ldx,
+              int32_t layout, int32_t dtype, int32_t axis,
+              void* workspace, size_t workspace_bytes,
+              void* counters, size_t counter_bytes, void* stream);
+size_t tilec_sum_workspace_bytes(int64_t R, int64_t C, int32_t layout,
+                                 int32_t dtype, int32_t axis);
+size_t tilec_sum_counter_bytes(int64_t R, int64_t C, int32_t layout,
+                               int32_t dtype, int32_t axis);
+
 /* Message describing the last failure on this thread ("" if none). */
 const char* tilec_last_error(void);
 

@@ -13,13 +13,18 @@ Contents
     (tilec/language.py:16-18), `plan`, `_blocks`, `mm_configs`
     (tilec/ext.py:10,29-51) and the tuner's shape generator
     (tilec/tune.py:54-65);
-  * the seeded input generators and error metrics every parity check uses.
+  * the seeded input generators and error metrics every parity check uses;
+  * numpy restatements of the reduction `tl.sum` (row and column sums).
 
 Pinning (tests/test_oracle.py): see the header of matmul_oracle.c.  The
 integer helpers are pinned by the reference's one known answer
 (cdiv(5000, 4096) == 2, tilec/language.py:17), by hand-derived values
 (plan(300) == (1024, 1), plan(5000) == (4096, 2), ...) and by brute-force
 characterisations (smallest power of 4, the two filter rules of mm_configs).
+The sums are pinned by the known answer of the reference's own example
+(kernel1.py:18-27: the row sums of arange(32).reshape(4, 8), which it checks
+against numpy's x.sum(axis=1)), by brute-force loops on small inputs and by
+the invariant that row and column sums share one total.
 """
 
 import ctypes
@@ -243,3 +248,40 @@ def ref_tune_shapes(n=500, seed=0):
         if M1 * N * M2 <= 1 << 31 and M1 * N <= 1 << 25 and N * M2 <= 1 << 25:
             out.add((M1, N, M2))
     return sorted(out, key=lambda s: s[0] * s[1] * s[2])
+
+
+# ---------------------------------------------------------------------------
+# Reductions.  The reference plans `tl.sum` (README.md:88) and shows it as
+# the `row_sum` kernel (kernel1.py:8-15): out[r] = tl.sum(x[r, :]) over a
+# row-major [R, C] fp32 matrix.  Restated in float64 (the parity reference)
+# and as the literal fp32 left-to-right sum of one thread (the CPU baseline).
+# ---------------------------------------------------------------------------
+
+def sum_f64(x, axis=1):
+    """Row (axis=1) or column (axis=0) sums of a 2-D array, in float64."""
+    x = np.asarray(x)
+    assert x.ndim == 2 and axis in (0, 1)
+    return x.astype(np.float64).sum(axis=axis)
+
+
+def sum_abs_f64(x, axis=1):
+    """sum |x| along the same axis: the scale of a sum's rounding error."""
+    return np.abs(np.asarray(x).astype(np.float64)).sum(axis=axis)
+
+
+def row_sum_f32_seq(x):
+    """kernel1.py:14 as one thread runs it: for each row, acc = 0.0f, then
+    acc += x[r][c] for c = 0 .. C-1 in fp32 (vectorised over rows)."""
+    x = np.asarray(x, dtype=np.float32)
+    acc = np.zeros(x.shape[0], dtype=np.float32)
+    for c in range(x.shape[1]):
+        acc += x[:, c]
+    return acc
+
+
+def sum_error_ok(got, x, axis=1, rel=2e-6):
+    """Per output: |got - sum| <= rel * sum |x| (fp32 accumulation in any
+    order; rel covers chains of a few hundred fp32 additions)."""
+    ref = sum_f64(x, axis)
+    bound = rel * sum_abs_f64(x, axis) + 1e-30
+    return bool(np.all(np.abs(np.asarray(got, np.float64) - ref) <= bound))

@@ -365,3 +365,58 @@ def test_operand_layouts_read_in_place():
     assert ext.layout_of(a, a.t()) == _lib.X2_COL_MAJOR
     assert ext.layout_of(a.t(), a) == _lib.X1_COL_MAJOR
     assert ext.layout_of(a.t(), a.t().t()) == _lib.X1_COL_MAJOR
+
+
+# ---------------------------------------------------------------------------
+# Sums: C ABI validation and split geometry (no device calls)
+# ---------------------------------------------------------------------------
+
+def _sum_call(R=8, C=8, ldx=None, layout=0, dtype=0, axis=1, ws=None, ws_bytes=0, cnt=None, cnt_bytes=0,
+              x=16, out=16):
+    # Non-null dummy pointers: every case must fail (or finish) before launch.
+    L = _lib.lib()
+    return L.tilec_sum(x, out, R, C, ldx if ldx is not None else (R if layout else C), layout, dtype, axis,
+                       ws, ws_bytes, cnt, cnt_bytes, None)
+
+
+def test_sum_abi_rejects_bad_arguments_before_launch():
+    assert _sum_call(dtype=5) == _lib.ERR_TYPE
+    assert _sum_call(axis=2) == _lib.ERR_VALUE and "axis" in _lib.last_error()
+    assert _sum_call(layout=_lib.X2_COL_MAJOR) == _lib.ERR_VALUE
+    assert _sum_call(R=-1) == _lib.ERR_VALUE
+    assert _sum_call(ldx=3) == _lib.ERR_VALUE and "ldx=3 < C=8" in _lib.last_error()
+    assert _sum_call(C=4, ldx=3, layout=_lib.X1_COL_MAJOR) == _lib.ERR_VALUE and "ldx=3 < R=8" in _lib.last_error()
+    assert _sum_call(out=None) == _lib.ERR_VALUE
+    assert _sum_call(x=None) == _lib.ERR_VALUE
+    # no outputs: nothing to do, no device access
+    assert _sum_call(R=0, x=None, out=None) == _lib.OK
+    assert _sum_call(C=0, axis=0, x=None, out=None) == _lib.OK
+    # a few long rows split their columns: workspace, then zeroed counters
+    assert _sum_call(R=4, C=1 << 20) == _lib.ERR_WORKSPACE and "workspace" in _lib.last_error()
+    assert _sum_call(R=4, C=1 << 20, ws=16, ws_bytes=1 << 30) == _lib.ERR_WORKSPACE
+    assert "counters" in _lib.last_error()
+    # rows too long for 32-bit offsets
+    assert _sum_call(R=1, C=(1 << 29) + 1, ldx=(1 << 29) + 1) == _lib.ERR_UNSUPPORTED
+
+
+def test_sum_geometry():
+    L = _lib.lib()
+    ws = L.tilec_sum_workspace_bytes
+    cnt = L.tilec_sum_counter_bytes
+    # 4096 rows of 4096: a wave per row, 1024 workgroups: no split
+    assert ws(4096, 4096, 0, 0, 1) == 0 and cnt(4096, 4096, 0, 0, 1) == 0
+    # 4 long rows: one workgroup of rows, columns split; partials of 256 floats
+    # per workgroup and split, one counter line per workgroup
+    w = ws(4, 1 << 20, 0, 0, 1)
+    assert w > 0 and w % (256 * 4) == 0 and cnt(4, 1 << 20, 0, 0, 1) == 256
+    # column sums of 4096 x 4096: 64 slabs of 64 columns, rows split 8 ways
+    assert ws(4096, 4096, 0, 0, 0) == 8 * 64 * 256 * 4 and cnt(4096, 4096, 0, 0, 0) == 64 * 256
+    # bf16 slabs are 128 columns wide
+    assert cnt(4096, 4096, 0, 1, 0) == 32 * 256
+    # a column-major matrix sums like the row-major transpose along the other axis
+    assert ws(1 << 20, 4, _lib.X1_COL_MAJOR, 0, 0) == w
+    assert ws(4096, 4096, _lib.X1_COL_MAJOR, 0, 1) == ws(4096, 4096, 0, 0, 0)
+    # short rows (C <= 16 fp32): one lane per row, 256 rows per workgroup
+    assert ws(1 << 20, 8, 0, 0, 1) == 0
+    # invalid arguments size nothing
+    assert ws(4, 1 << 20, 0, 0, 7) == 0

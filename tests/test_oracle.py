@@ -235,3 +235,43 @@ def test_ref_tune_shapes_properties():
         assert M1 * N * M2 <= 1 << 31 and M1 * N <= 1 << 25 and N * M2 <= 1 << 25
         assert 2 ** 7 - 1 <= M1 <= 2 ** 13 + 1 and 2 ** 5 - 1 <= M2 <= 2 ** 12 + 1
     assert O.ref_tune_shapes(50, seed=1) == O.ref_tune_shapes(50, seed=1)
+
+
+# ---------------------------------------------------------------------------
+# Sums (tl.sum, kernel1.py:8-15)
+# ---------------------------------------------------------------------------
+
+def test_sum_reference_example_known_answer():
+    """kernel1.py:18-27 sums the rows of arange(32).reshape(4, 8) and checks
+    them against numpy's x.sum(axis=1): row r holds 8r .. 8r+7, so its sum
+    is 64r + 28; column c holds c, 8+c, 16+c, 24+c, so its sum is 48 + 4c."""
+    x = np.arange(32, dtype=np.float32).reshape(4, 8)
+    np.testing.assert_array_equal(O.sum_f64(x, 1), [28, 92, 156, 220])
+    np.testing.assert_array_equal(O.sum_f64(x, 0), [48 + 4 * c for c in range(8)])
+    np.testing.assert_array_equal(O.row_sum_f32_seq(x), [28, 92, 156, 220])
+
+
+def test_sum_matches_brute_force_loops():
+    for i, (r, c) in enumerate([(1, 1), (3, 7), (5, 1), (1, 33), (17, 65)]):
+        x = O.normal((r, c), 900 + i)
+        rows = [math.fsum(float(x[a, b]) for b in range(c)) for a in range(r)]
+        cols = [math.fsum(float(x[a, b]) for a in range(r)) for b in range(c)]
+        np.testing.assert_allclose(O.sum_f64(x, 1), rows, rtol=1e-13, atol=1e-13)
+        np.testing.assert_allclose(O.sum_f64(x, 0), cols, rtol=1e-13, atol=1e-13)
+        seq = O.row_sum_f32_seq(x)
+        for a in range(r):  # the fp32 loop, element by element
+            acc = np.float32(0)
+            for b in range(c):
+                acc = np.float32(acc + x[a, b])
+            assert seq[a] == acc
+
+
+def test_sum_invariants_and_error_bound():
+    x = O.normal((300, 257), 910)
+    assert math.isclose(O.sum_f64(x, 1).sum(), O.sum_f64(x, 0).sum(), rel_tol=1e-12, abs_tol=1e-9)
+    y = O.normal((300, 257), 911)
+    np.testing.assert_allclose(O.sum_f64(x + y, 1), O.sum_f64(x, 1) + O.sum_f64(y, 1), rtol=1e-6, atol=1e-5)
+    assert O.sum_error_ok(O.row_sum_f32_seq(x), x, 1)
+    # the bound rejects a dropped element (a plausible off-by-one)
+    assert not O.sum_error_ok(O.row_sum_f32_seq(x[:, :-1]), x, 1)
+    assert not O.sum_error_ok(O.sum_f64(x, 1) + 1e-3, x, 1)

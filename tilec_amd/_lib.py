@@ -28,6 +28,9 @@ SIGNATURES = {
                                     _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp]),
     "tilec_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
     "tilec_matmul_counter_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
+    "tilec_sum": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp]),
+    "tilec_sum_workspace_bytes": (_sz, [_i64, _i64, _i32, _i32, _i32]),
+    "tilec_sum_counter_bytes": (_sz, [_i64, _i64, _i32, _i32, _i32]),
     "tilec_select_variant": (_i32, [_i64, _i64, _i64, _i32]),
     "tilec_auto_split_k": (_i32, [_i64, _i64, _i64, _i32, _i32]),
     "tilec_num_variants": (_i32, []),

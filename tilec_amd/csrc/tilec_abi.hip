@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -21,6 +22,15 @@ const VariantDesc* gemm_bf16_variants(int* count);
 size_t skinny_counter_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 size_t skinny_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 int64_t skinny_effective_splits(int64_t N, int64_t K, int split_k);
+struct ReduceGeom {
+  int64_t cells, splits, span;
+  int lpr;
+};
+ReduceGeom reduce_geom(int64_t R, int64_t C, int esz, int axis);
+size_t reduce_workspace_bytes(const ReduceGeom& g);
+size_t reduce_counter_bytes(const ReduceGeom& g);
+hipError_t launch_reduce(const void* x, float* out, int64_t R, int64_t C, int64_t ld, int dtype, int axis, float* ws,
+                         unsigned* counters, hipStream_t stream);
 }  // namespace tilec
 
 using namespace tilec;
@@ -208,9 +218,86 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
   return TILEC_OK;
 }
 
+// Sums: validate, then express a column-major x as the row-major view of its
+// transpose (swap R and C, flip the axis).  The kernels address a row of x
+// (axis 1) or 16 rows of it (axis 0) with 32-bit byte offsets, and their
+// split partials likewise.
+struct SumPlan {
+  int64_t R, C;
+  int axis, esz;
+  ReduceGeom g;
+};
+
+int sum_plan(int64_t R, int64_t C, int64_t ldx, int32_t layout, int32_t dtype, int32_t axis, SumPlan* p) {
+  if (dtype != TILEC_F32 && dtype != TILEC_BF16)
+    return fail(TILEC_ERR_TYPE, "tilec: unsupported dtype code %d (use float32 or bfloat16)", dtype);
+  if (R < 0 || C < 0 || R > kMaxDim || C > kMaxDim)
+    return fail(TILEC_ERR_VALUE, "tilec: bad shape R=%lld C=%lld", (long long)R, (long long)C);
+  if (axis != 0 && axis != 1) return fail(TILEC_ERR_VALUE, "tilec: axis must be 0 or 1 (got %d)", axis);
+  if (layout & ~TILEC_X1_COL_MAJOR) return fail(TILEC_ERR_VALUE, "tilec: unknown layout bits 0x%x", layout);
+  const bool col = layout & TILEC_X1_COL_MAJOR;
+  p->R = col ? C : R;
+  p->C = col ? R : C;
+  p->axis = col ? 1 - axis : axis;
+  p->esz = dtype == TILEC_BF16 ? 2 : 4;
+  if (ldx > 0 && ldx >= (int64_t(1) << 40)) return fail(TILEC_ERR_VALUE, "tilec: ldx=%lld is too large", (long long)ldx);
+  if (p->axis == 1 && p->C * p->esz >= (int64_t(1) << 31) - 64)
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: rows of %lld elements are too long to sum", (long long)p->C);
+  if (p->axis == 0 && ldx > 0 && 16 * ldx * p->esz >= (int64_t(1) << 31) - 64)
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: a row stride of %lld elements is too large for column sums",
+                (long long)ldx);
+  p->g = reduce_geom(p->R, p->C, p->esz, p->axis);
+  if (p->g.splits > 65535 || p->g.cells > 0x7FFFFFFF ||
+      (int64_t)reduce_workspace_bytes(p->g) >= (int64_t(1) << 31))
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: sum of %lld x %lld is too large", (long long)R, (long long)C);
+  return TILEC_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int tilec_sum(const void* x, float* out, int64_t R, int64_t C, int64_t ldx, int32_t layout, int32_t dtype,
+              int32_t axis, void* workspace, size_t workspace_bytes, void* counters, size_t counter_bytes,
+              void* stream) {
+  g_err[0] = 0;
+  SumPlan p;
+  const int rc = sum_plan(R, C, ldx, layout, dtype, axis, &p);
+  if (rc != TILEC_OK) return rc;
+  const int64_t outputs = axis == 1 ? R : C;
+  if (outputs == 0) return TILEC_OK;
+  if (out == nullptr) return fail(TILEC_ERR_VALUE, "tilec: out is NULL");
+  if (R > 0 && C > 0) {
+    if (x == nullptr) return fail(TILEC_ERR_VALUE, "tilec: x is NULL");
+    if (ldx < p.C)
+      return fail(TILEC_ERR_VALUE, "tilec: ldx=%lld < %s=%lld", (long long)ldx,
+                  (layout & TILEC_X1_COL_MAJOR) ? "R" : "C", (long long)p.C);
+  }
+  const size_t need = reduce_workspace_bytes(p.g), need_cnt = reduce_counter_bytes(p.g);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(TILEC_ERR_WORKSPACE, "tilec: sum needs %zu workspace bytes (got %zu)", need,
+                workspace == nullptr ? (size_t)0 : workspace_bytes);
+  if (need_cnt > 0 && (counters == nullptr || counter_bytes < need_cnt))
+    return fail(TILEC_ERR_WORKSPACE, "tilec: sum needs %zu bytes of counters (got %zu)", need_cnt,
+                counters == nullptr ? (size_t)0 : counter_bytes);
+  const hipError_t e = launch_reduce(x, out, p.R, p.C, ldx > 0 ? ldx : std::max<int64_t>(p.C, 1), dtype, p.axis,
+                                     static_cast<float*>(workspace), static_cast<unsigned*>(counters),
+                                     static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(TILEC_ERR_HIP, "tilec: launching the sum failed: %s", hipGetErrorString(e));
+  return TILEC_OK;
+}
+
+size_t tilec_sum_workspace_bytes(int64_t R, int64_t C, int32_t layout, int32_t dtype, int32_t axis) {
+  SumPlan p;
+  if (sum_plan(R, C, 0, layout, dtype, axis, &p) != TILEC_OK || (axis == 1 ? R : C) == 0) return 0;
+  return reduce_workspace_bytes(p.g);
+}
+
+size_t tilec_sum_counter_bytes(int64_t R, int64_t C, int32_t layout, int32_t dtype, int32_t axis) {
+  SumPlan p;
+  if (sum_plan(R, C, 0, layout, dtype, axis, &p) != TILEC_OK || (axis == 1 ? R : C) == 0) return 0;
+  return reduce_counter_bytes(p.g);
+}
 
 int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t N, int64_t K, int64_t ldx1,
                  int64_t ldx2, int64_t ldo, int32_t layout, int32_t dtype, int32_t variant, int32_t split_k,

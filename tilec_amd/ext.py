@@ -1,4 +1,4 @@
-"""tilec ops on PyTorch-ROCm tensors: `matrix_mul(x1, x2)`.
+"""tilec ops on PyTorch-ROCm tensors: `matrix_mul(x1, x2)` and `sum(x, axis)`.
 
 Host code mirroring the reference's op module (tilec/ext.py): the same public
 call, the same shape error, the same `.contiguous()` semantics and a freshly
@@ -9,6 +9,7 @@ libtilec_hip.so instead of a JIT-compiled Metal tile kernel.
     x1 = torch.randn(512, 4096, device="cuda")
     x2 = torch.randn(4096, 64, device="cuda")
     out = tilec.ext.matrix_mul(x1, x2)
+    rows = tilec.ext.sum(x1, axis=1)       # [512] fp32 row sums
 
 Kernel choice per shape comes from `tune.pick` (the shape→config model trained
 on MI355X), falling back to the library's built-in rule when no model is
@@ -22,7 +23,7 @@ from . import _lib
 from .language import cdiv
 
 __all__ = [
-    "matrix_mul", "_matrix_mul_tiled", "cdiv", "plan", "mm_configs", "_blocks",
+    "matrix_mul", "_matrix_mul_tiled", "sum", "cdiv", "plan", "mm_configs", "_blocks",
     "MAX_BLOCK", "SPLITS", "JOINS", "BLOCKS", "hip_configs", "workspace_for", "counters_for",
 ]
 
@@ -317,3 +318,48 @@ def _matrix_mul_tiled(x1, x2, BM=64, BN=64, BK=16):
         raise ValueError(f"_matrix_mul_tiled: no compiled tile BM={BM} BN={BN} BK={BK} "
                          f"for {x1.dtype}; available (BM, BN, BK): {have}")
     return _launch(x1, x2, M, K, N, chosen[0]["id"], 1)
+
+
+def sum(x, axis=1):
+    """Row sums (axis=1: out[r] = sum_c x[r, c], shape [R]) or column sums
+    (axis=0: out[c] = sum_r x[r, c], shape [C]) of a 2-D float32 or bfloat16
+    tensor on the GPU, accumulated and returned in float32.  A 1-D x is one
+    row.
+
+    The reduction the reference plans as `tl.sum` (README.md:88) and shows
+    as the `row_sum` kernel, `out[r] = tl.sum(x[r, :])`, with the op-level
+    spelling `tl.ext.sum(x, axis=1)` (kernel1.py:8-15).  Row- and
+    column-major views are read in place; other strided views are copied
+    first.  Long reductions with few outputs split across workgroups and
+    combine in a fixed order: results are deterministic.
+    """
+    if x.dim() == 1:
+        x = x.unsqueeze(0)
+    if x.dim() != 2:
+        raise ValueError(f"sum: expected a 1-D or 2-D tensor, got shape {tuple(x.shape)}")
+    if axis not in (0, 1, -1, -2):
+        raise ValueError(f"sum: axis must be 0 or 1 (got {axis})")
+    axis = axis % 2
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"unsupported tensor of dtype {x.dtype} (use float32 or bfloat16)")
+    if x.device.type != "cuda":
+        raise TypeError(f"sum needs a tensor on a ROCm GPU (got {x.device})")
+    R, C = x.shape
+    out = torch.empty((R if axis == 1 else C,), dtype=torch.float32, device=x.device)
+    if out.numel() == 0:
+        return out
+    t, ld, col = _operand(x, R, C)
+    layout = _lib.X1_COL_MAJOR if col else 0
+    dtype = _lib.F32 if x.dtype == torch.float32 else _lib.BF16
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    ws_ptr, ws_bytes, cnt_ptr, cnt_bytes = None, 0, None, 0
+    need = L.tilec_sum_workspace_bytes(R, C, layout, dtype, axis)
+    if need:
+        ws = workspace_for(x.device, stream, need)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+        cnt = counters_for(x.device, stream, L.tilec_sum_counter_bytes(R, C, layout, dtype, axis))
+        cnt_ptr, cnt_bytes = cnt.data_ptr(), cnt.numel()
+    _lib.check(L.tilec_sum(t.data_ptr(), out.data_ptr(), R, C, ld, layout, dtype, axis,
+                           ws_ptr, ws_bytes, cnt_ptr, cnt_bytes, stream))
+    return out
