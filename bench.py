@@ -19,6 +19,8 @@ warmup steps.  Extra objects in the same line:
   layouts      — transposed operands read in place: x @ W.T GEMV (weight
                  W [N, K] row-major) as in `skinny`, and the 4096^3 fp32 /
                  8192^3 bf16 GEMMs with x1, x2 or both column-major
+  reduce       — row and column sums (ext.sum, the reference's tl.sum) in
+                 HBM GB/s, graph-replayed over rotating inputs
   cpu_baseline — the oracle's tiled C restatement of the reference kernel
                  (oracle/matmul_oracle.c, OpenMP) on a bounded row sample of
                  the same 4096^3 problem, on this box's host cores; plus
@@ -47,7 +49,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the skinny and bf16 sections")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
-    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "copy"],
+    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "copy"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -247,6 +249,52 @@ def bench_configs(reps=20):
     return out
 
 
+REDUCE_CASES = (
+    # (name, R, C, dtype, axis): the config-1 x2 summed both ways, a few long
+    # rows (split columns) and a tall, narrow bf16 matrix (split rows)
+    ("rows_4096x4096_f32", 4096, 4096, "f32", 1),
+    ("cols_4096x4096_f32", 4096, 4096, "f32", 0),
+    ("rows_8x4194304_f32", 8, 1 << 22, "f32", 1),
+    ("rows_4096x8192_bf16", 4096, 8192, "bf16", 1),
+    ("cols_1048576x64_bf16", 1 << 20, 64, "bf16", 0),
+)
+
+
+def bench_reduce(reps=8):
+    """Row and column sums (ext.sum): HBM GB/s from graph-replayed calls over
+    rotating inputs (>= 512 MB in total, beyond the Infinity Cache)."""
+    import torch
+    from oracle import oracle as O
+    from tilec_amd import ext
+    out = {}
+    for i, (name, R, C, dtype, axis) in enumerate(REDUCE_CASES):
+        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+        esz = 4 if dtype == "f32" else 2
+        nbuf = max(2, (512 << 20) // (esz * R * C))
+        xs = [torch.from_numpy(O.normal((R, C), 2000 + 10 * i + j)).to(tdt).cuda() for j in range(nbuf)]
+        for x in xs:  # workspace exists before capture
+            ext.sum(x, axis)
+        torch.cuda.synchronize()
+        calls = 4 * nbuf
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            ext.sum(xs[0], axis)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                outs = [ext.sum(xs[j % nbuf], axis) for j in range(calls)]
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            ms = timed(g.replay, reps, 2, stream=s) / calls
+        del outs, xs
+        nbytes = esz * R * C + 4 * (R if axis == 1 else C)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes)
+        log(f"sum {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM:.1f}% of HBM)")
+    return out
+
+
 def bench_copy(nbytes=256 << 20, reps=10):
     """A plain device-to-device copy of known size: what FETCH_SIZE and
     WRITE_SIZE read for it calibrates those counters."""
@@ -335,7 +383,8 @@ def main():
 
     if args.only:
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
-               "configs": bench_configs, "layouts": bench_layouts, "copy": bench_copy}[args.only]()
+               "configs": bench_configs, "layouts": bench_layouts, "reduce": bench_reduce,
+               "copy": bench_copy}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return
 
@@ -346,6 +395,7 @@ def main():
         extra["bf16_8192"] = bench_bf16()
         extra["configs"] = bench_configs()
         extra["layouts"] = bench_layouts()
+        extra["reduce"] = bench_reduce()
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
 
     rec = {

@@ -145,7 +145,8 @@ __global__ __launch_bounds__(kNT) void row_sum_kernel(const T* __restrict__ x, f
   constexpr int U = 4;  // groups in flight per lane
   __shared__ float red[kNT];
   __shared__ int last_flag;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int rpw = 64 / lpr, rpg = kWaves * rpw;
   const int slot = wave * rpw + lane / lpr;  // row within the workgroup
   const int sub = lane & (lpr - 1);
@@ -154,12 +155,15 @@ __global__ __launch_bounds__(kNT) void row_sum_kernel(const T* __restrict__ x, f
   const int cbeg = split * chunk;
   const int n = r < R ? max(0, min(C, cbeg + chunk) - cbeg) : 0;  // this split's columns of the row
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const BufRsrc rs = make_rsrc(x + (int64_t)min(r, R - 1) * ld + cbeg);
+  // One resource per wave, at its first row (buffer resources are
+  // wave-uniform); a lane's row is a byte offset from it.
+  const BufRsrc rs = make_rsrc(x + (int64_t)(blockIdx.x * rpg + wave * rpw) * ld + cbeg);
+  const uint32_t row_off = (uint32_t)(lane / lpr) * (uint32_t)ld * (uint32_t)sizeof(T);
   const int step = E * lpr;
   for (int c0 = E * sub; c0 < n; c0 += U * step) {
     i32x4 w[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = load_group<T, VEC>(rs, 0u, c0 + u * step, n);
+    for (int u = 0; u < U; ++u) w[u] = load_group<T, VEC>(rs, row_off, c0 + u * step, n);
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -192,7 +196,8 @@ __global__ __launch_bounds__(kNT) void col_sum_kernel(const T* __restrict__ x, f
   constexpr int UB = 2;  // 16-row blocks in flight per wave: 4 UB groups per lane
   __shared__ float red[kWaves * SLAB > kNT ? kWaves * SLAB : kNT];
   __shared__ int last_flag;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int r4 = lane >> 4, q = lane & 15;
   const int slab = blockIdx.x, split = blockIdx.y, S = gridDim.y;
   const int n0 = slab * SLAB;
@@ -210,13 +215,16 @@ __global__ __launch_bounds__(kNT) void col_sum_kernel(const T* __restrict__ x, f
 #pragma unroll
     for (int j = 0; j < UB; ++j) {
       const int b = b0 + j * kWaves;  // may be past the split: its rows load nothing
-      // Resource at the block's first row; rows past the split get n = 0.
-      const BufRsrc rs = make_rsrc(x + (int64_t)(rbeg + min(16 * b, nrows)) * ld + n0 + E * q);
+      // One resource per wave and block, at the block's first row and the
+      // slab's first column (wave-uniform); a lane's row and columns are a
+      // byte offset from it.  Rows past the split get n = 0.
+      const BufRsrc rs = make_rsrc(x + (int64_t)(rbeg + min(16 * b, nrows)) * ld + n0);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int row = 4 * r4 + u;  // within the block
         const bool ok = 16 * b + row < nrows;
-        w[j][u] = load_group<T, VEC>(rs, (uint32_t)row * (uint32_t)ld * (uint32_t)sizeof(T), 0, ok ? cn : 0);
+        const uint32_t off = ((uint32_t)row * (uint32_t)ld + (uint32_t)(E * q)) * (uint32_t)sizeof(T);
+        w[j][u] = load_group<T, VEC>(rs, off, 0, ok ? cn : 0);
       }
     }
 #pragma unroll

@@ -219,9 +219,9 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
 }
 
 // Sums: validate, then express a column-major x as the row-major view of its
-// transpose (swap R and C, flip the axis).  The kernels address a row of x
-// (axis 1) or 16 rows of it (axis 0) with 32-bit byte offsets, and their
-// split partials likewise.
+// transpose (swap R and C, flip the axis).  The kernels address the rows of
+// one wave (axis 1: 64 / lpr rows) or one 16-row block (axis 0) with 32-bit
+// byte offsets, and their split partials likewise.
 struct SumPlan {
   int64_t R, C;
   int axis, esz;
@@ -247,6 +247,10 @@ int sum_plan(int64_t R, int64_t C, int64_t ldx, int32_t layout, int32_t dtype, i
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: a row stride of %lld elements is too large for column sums",
                 (long long)ldx);
   p->g = reduce_geom(p->R, p->C, p->esz, p->axis);
+  // Row sums address a wave's 64 / lpr rows from its first one.
+  if (p->axis == 1 && ldx > 0 && (64 / p->g.lpr) * ldx * p->esz + p->C * p->esz >= (int64_t(1) << 31) - 64)
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: a row stride of %lld elements is too large for sums of short rows",
+                (long long)ldx);
   if (p->g.splits > 65535 || p->g.cells > 0x7FFFFFFF ||
       (int64_t)reduce_workspace_bytes(p->g) >= (int64_t(1) << 31))
     return fail(TILEC_ERR_UNSUPPORTED, "tilec: sum of %lld x %lld is too large", (long long)R, (long long)C);
