@@ -420,3 +420,21 @@ def test_sum_geometry():
     assert ws(1 << 20, 8, 0, 0, 1) == 0
     # invalid arguments size nothing
     assert ws(4, 1 << 20, 0, 0, 7) == 0
+
+
+def test_prep_variants_workspace_and_splits():
+    """*_kc variants hold transposed copies of both operands in the workspace
+    (256-byte aligned, sized for any layout) and never split K."""
+    L = _lib.lib()
+    v = _lib.variant_id("gemm_bf16_256x256x64_r2_kc")
+    M, N, K = 1000, 520, 3000
+    a = (M * K * 2 + 255) // 256 * 256
+    b = (K * N * 2 + 255) // 256 * 256
+    assert L.tilec_matmul_workspace_bytes(M, N, K, _lib.BF16, v, 1) == a + b
+    assert L.tilec_matmul_counter_bytes(M, N, K, _lib.BF16, v, 1) == 0
+    assert L.tilec_matmul_workspace_bytes(M, N, 0, _lib.BF16, v, 1) == 0
+    assert L.tilec_auto_split_k(64, 64, 4096, _lib.BF16, v) == 1
+    assert _call(M=64, N=64, K=4096, dtype=_lib.BF16, variant=v, split=2) == _lib.ERR_UNSUPPORTED
+    assert _call(M=64, N=64, K=4096, dtype=_lib.BF16, variant=v, split=1) == _lib.ERR_WORKSPACE
+    kc = [c for c in ext.hip_configs(64, 4096, 64, "bf16") if c[0].endswith("_kc")]
+    assert kc and all(s == 1 for _, s in kc)

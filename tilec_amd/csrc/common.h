@@ -42,7 +42,19 @@ struct VariantDesc {
   int unroll;
   // Launch on args.stream; returns hipError_t.
   hipError_t (*launch)(const MatmulArgs&);
+  // 1: the launch first copies each operand that is not k-contiguous into
+  // the workspace transposed (prep_workspace_bytes), then runs the tile GEMM
+  // on k-contiguous operands; such variants never split K.
+  int prep = 0;
 };
+
+// Workspace of a prep variant: a transposed copy of x1 (M x K) and of x2
+// (K x N), bf16, each at a 256-byte aligned offset (whichever the layout
+// needs; sized for both).
+inline size_t prep_offset_b(int64_t M, int64_t K) { return (size_t)((M * K * 2 + 255) / 256 * 256); }
+inline size_t prep_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return prep_offset_b(M, K) + (size_t)((K * N * 2 + 255) / 256 * 256);
+}
 
 // ---------------------------------------------------------------------------
 // MFMA wrappers.  Lane layouts (lane l of 64):

@@ -98,12 +98,13 @@ constexpr int64_t kGemmMaxPartialBytes = (int64_t(1) << 31) - 1;
 int64_t gemm_tiles(const VariantDesc* d, int64_t M, int64_t N) { return cdiv(M, d->bm) * cdiv(N, d->bn); }
 
 size_t gemm_workspace_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K, int s) {
+  if (d->prep) return K > 0 ? prep_workspace_bytes(M, N, K) : 0;
   const SplitGeom g = gemm_split_geom(K, d->bk, s);
   if (g.splits <= 1) return 0;
   return (size_t)g.splits * gemm_tiles(d, M, N) * d->bm * d->bn * sizeof(float);
 }
 size_t gemm_counter_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K, int s) {
-  if (gemm_split_geom(K, d->bk, s).splits <= 1) return 0;
+  if (d->prep || gemm_split_geom(K, d->bk, s).splits <= 1) return 0;
   return (size_t)gemm_tiles(d, M, N) * kSplitCounterStride * sizeof(unsigned);
 }
 
@@ -143,7 +144,7 @@ int auto_split(const VariantDesc* d, int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 1;
   if (d->family == TILEC_FAMILY_GEMM) {
     const int64_t tiles = gemm_tiles(d, M, N);
-    if (tiles >= kCUs || !tile_can_split(d->bm, d->bn, d->waves)) return 1;
+    if (tiles >= kCUs || d->prep || !tile_can_split(d->bm, d->bn, d->waves)) return 1;
     int64_t s = cdiv(kCUs, tiles);
     const int64_t s_max = cdiv(K, d->bk) / 4;
     if (s > s_max) s = s_max;
@@ -193,8 +194,10 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
   int s = split_k == 0 ? auto_split(d, M, N, K) : split_k;
   if (d->family == TILEC_FAMILY_GEMM) {
     const SplitGeom g = gemm_split_geom(K, d->bk, s);
-    if (g.splits > 1 && !tile_can_split(d->bm, d->bn, d->waves))
+    if (g.splits > 1 && (d->prep || !tile_can_split(d->bm, d->bn, d->waves)))
       return fail(TILEC_ERR_UNSUPPORTED, "tilec: variant %s does not split K (split_k=%d)", d->name, s);
+    if (d->prep && M * K * 2 + K * N * 2 >= (int64_t(1) << 40))
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: operands too large to transpose", d->name);
     if (g.splits > 65535)
       return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
     if (g.splits > 1 && (int64_t)gemm_workspace_bytes(d, M, N, K, s) > kGemmMaxPartialBytes)

@@ -118,10 +118,17 @@ _GEMM_SPLITS = (2, 4, 8, 16)
 SPLIT_MAX_ACC_PER_THREAD = 64  # tilec_amd/csrc/common.h, kSplitMaxAccPerThread
 
 
+def prep_variant(v):
+    """Variants named *_kc transpose each operand that is not k-contiguous
+    into the workspace before the GEMM (csrc/common.h, VariantDesc::prep);
+    they never split K."""
+    return v["name"].endswith("_kc")
+
+
 def tile_can_split(v):
     """Whether a tile-GEMM variant splits K (its threads hold at most 64
-    accumulators; csrc/common.h, tile_can_split)."""
-    return v["bm"] * v["bn"] <= SPLIT_MAX_ACC_PER_THREAD * 64 * v["waves"]
+    accumulators; csrc/common.h, tile_can_split; prep variants never do)."""
+    return not prep_variant(v) and v["bm"] * v["bn"] <= SPLIT_MAX_ACC_PER_THREAD * 64 * v["waves"]
 
 
 def _gemm_splits(K, split_k, bk):
