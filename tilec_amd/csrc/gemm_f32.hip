@@ -8,7 +8,9 @@
 // that starts at zero, a K loop in steps of BK over masked tiles of A and B
 // (`other=0.0`), and a masked store.  What runs underneath is MI355X-native:
 //   * 64-wide waves arranged WM x WN, each owning a (BM/WM) x (BN/WN) block of
-//     32x32 MFMA accumulators held in registers for the whole K loop;
+//     32x32 MFMA accumulators held in registers for the whole K loop (8-wave
+//     grids keep two waves per SIMD on one large tile: their MFMAs cover each
+//     other's barrier and load waits);
 //   * A and B tiles double-buffered in LDS with one barrier per K step; the
 //     next tile's global loads are issued before the current tile's MFMAs;
 //   * A stored k-major in LDS (As[k][m]) so every MFMA operand read is one
@@ -340,6 +342,14 @@ const VariantDesc* gemm_f32_variants(int* count) {
        launch_gemm_f32<128, 64, 16, 2, 2>},
       {"gemm_f32_64x64x16_w2x2", TILEC_FAMILY_GEMM, TILEC_F32, 64, 64, 16, 4, 0, 1,
        launch_gemm_f32<64, 64, 16, 2, 2>},
+      {"gemm_f32_256x256x16_w2x4", TILEC_FAMILY_GEMM, TILEC_F32, 256, 256, 16, 8, 0, 1,
+       launch_gemm_f32<256, 256, 16, 2, 4>},
+      {"gemm_f32_256x256x32_w2x4", TILEC_FAMILY_GEMM, TILEC_F32, 256, 256, 32, 8, 0, 1,
+       launch_gemm_f32<256, 256, 32, 2, 4>},
+      {"gemm_f32_128x128x16_w2x4", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 16, 8, 0, 1,
+       launch_gemm_f32<128, 128, 16, 2, 4>},
+      {"gemm_f32_128x128x32_w2x4", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 32, 8, 0, 1,
+       launch_gemm_f32<128, 128, 32, 2, 4>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

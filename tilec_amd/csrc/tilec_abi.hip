@@ -114,8 +114,8 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
   if (dtype == TILEC_F32) {
     if ((M <= 16 || small_output(M, N)) && cdiv(M, 16) <= kSkinnyMaxRowBlocks && skinny_fits(ldx1, ldx2, layout))
       return find("skinny_f32_w8_b1");
-    static const char* order[] = {"gemm_f32_256x256x16_w2x2", "gemm_f32_256x128x16_w2x2",
-                                  "gemm_f32_128x128x16_w2x2", "gemm_f32_128x64x16_w2x2"};
+    static const char* order[] = {"gemm_f32_256x256x32_w2x4", "gemm_f32_256x128x16_w2x2",
+                                  "gemm_f32_128x128x32_w2x4", "gemm_f32_128x64x16_w2x2"};
     for (const char* nm : order) {
       const int v = find(nm);
       const VariantDesc* d = table()[v];
