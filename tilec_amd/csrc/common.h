@@ -7,6 +7,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace tilec {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -109,6 +111,22 @@ __device__ __forceinline__ void store_f32x4_coherent(BufRsrc r, uint32_t off, f3
 }
 
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Kernels with more than 64 KiB of dynamic LDS need their limit raised once
+// per device (the attribute belongs to the kernel on the current device).
+// `done` is the caller's per-kernel record of devices already set up
+// (devices 0..63; others are set on every launch).
+inline hipError_t raise_lds_limit(const void* kernel, size_t lds, std::atomic<uint64_t>& done) {
+  if (lds <= 65536) return hipSuccess;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? uint64_t(1) << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
 
 // ---------------------------------------------------------------------------
 // Split-K combine for tile kernels (grid y = K splits).  Every workgroup of
