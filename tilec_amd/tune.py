@@ -72,6 +72,8 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
 
 
 GRAPH_BELOW_MS = 0.2   # calls shorter than this are timed from a replayed HIP graph
+SUSTAIN_CALLS = 4      # longer calls: back-to-back launches per timed sample
+SUSTAIN_WARMUP = 4     # ... after this many untimed back-to-back launches
 ROTATE_BYTES = 512 << 20  # rotate x2 over copies this large in total (> 256 MB Infinity Cache)
 
 
@@ -89,13 +91,15 @@ def operands_for(M, K, N, x2):
 
 
 def time_ms(x1, x2, config, best=None, reps=5, x2s=None):
-    """Median of `reps` device-timed runs after one warmup, with the early
+    """Median of `reps` device-timed samples after warmup, with the early
     exit of tilec/tune.py:35-51 when a probe run is over twice the best.
 
     Device time from HIP events.  A call shorter than GRAPH_BELOW_MS is timed
     as a replay of a captured HIP graph of several calls (cycling over `x2s`
     when given), so host launch overhead does not pollute it; the result is
-    the median replay time divided by the calls per replay."""
+    the median replay time divided by the calls per replay.  Longer calls
+    are timed as SUSTAIN_CALLS back-to-back launches per sample, after
+    SUSTAIN_WARMUP more, i.e. at the clock the chip holds under load."""
     import torch
     from . import ext
     x2s = x2s or [x2]
@@ -133,13 +137,21 @@ def time_ms(x1, x2, config, best=None, reps=5, x2s=None):
                 times.append(s.elapsed_time(e) / calls)
         del outs, graph
         return sorted(times)[reps // 2]
+    # Longer calls: back-to-back launches, as a loop of products issues them.
+    # MI355X holds its boost clock for a short burst but slows under sustained
+    # matrix-core load, by an amount that depends on the kernel (its LDS and
+    # memory traffic per flop) and the data; timing isolated launches would
+    # rank kernels for a regime no training or serving loop runs in.
+    for _ in range(SUSTAIN_WARMUP):
+        ext.matrix_mul(x1, x2, config)
     times = []
     for _ in range(reps):
         s.record()
-        ext.matrix_mul(x1, x2, config)
+        for _ in range(SUSTAIN_CALLS):
+            ext.matrix_mul(x1, x2, config)
         e.record()
         e.synchronize()
-        times.append(s.elapsed_time(e))
+        times.append(s.elapsed_time(e) / SUSTAIN_CALLS)
     return sorted(times)[reps // 2]
 
 
