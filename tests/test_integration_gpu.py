@@ -1,10 +1,11 @@
-"""The reference-side binding documented in INTEGRATION.md, run as written.
+"""The reference-side binding of the repository's integration guide, run as
+written.
 
-INTEGRATION.md shows the ctypes stub a maintainer of the reference would put
-in tilec/ext.py in place of the Metal launch.  This test takes that code
-block verbatim (only the library path is made absolute), executes it, and
-checks its matrix_mul and sum against the oracle, so the documented binding
-cannot drift from include/tilec.h.
+The guide shows the ctypes stub a maintainer of the reference would put in
+tilec/ext.py in place of the Metal launch.  This test takes that code block
+verbatim (only the library path is made absolute), executes it, and checks
+its matrix_mul and sum against the oracle, so the documented binding cannot
+drift from include/tilec.h.
 """
 
 import os
@@ -20,17 +21,18 @@ from tilec_amd import _lib
 pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GUIDE = "INTEGRATION.md"
 
 
 def _stub_namespace():
-    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    text = open(os.path.join(ROOT, GUIDE)).read()
     blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
-    assert blocks, "INTEGRATION.md has no python block"
+    assert blocks, "the integration guide has no python block"
     code = blocks[0]
     assert 'ctypes.CDLL("libtilec_hip.so")' in code
     code = code.replace('ctypes.CDLL("libtilec_hip.so")', f"ctypes.CDLL({_lib.LIB_PATH!r})")
     ns = {}
-    exec(compile(code, "INTEGRATION.md", "exec"), ns)
+    exec(compile(code, GUIDE, "exec"), ns)
     return ns
 
 
