@@ -21,6 +21,9 @@ warmup steps.  Extra objects in the same line:
                  8192^3 bf16 GEMMs with x1, x2 or both column-major
   reduce       — row and column sums (ext.sum, the reference's tl.sum) in
                  HBM GB/s, graph-replayed over rotating inputs
+  vendor_torch_mm — the square fp32, config-4 bf16 and GEMV cases through
+                 torch.mm (hipBLASLt / rocBLAS, fp32 result) on the same
+                 box, data and timing protocol, for reference
   cpu_baseline — the oracle's tiled C restatement of the reference kernel
                  (oracle/matmul_oracle.c, OpenMP) on a bounded row sample of
                  the same 4096^3 problem, on this box's host cores; plus
@@ -49,7 +52,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the skinny and bf16 sections")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
-    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "copy"],
+    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "vendor", "copy"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -101,24 +104,26 @@ def bench_square(args):
     return dict(ms=ms, tflops=tflops, config=cfg)
 
 
-def _gemv(x1, x2s, steps):
-    """us per launch of x1 @ x2s[i] over rotating x2 buffers, launches
-    replayed from a HIP graph (an ~8 us kernel is not host-bound)."""
+def _gemv(x1, x2s, steps, mm=None):
+    """us per launch of mm(x1, x2s[i]) (default ext.matrix_mul) over rotating
+    x2 buffers, launches replayed from a HIP graph (an ~8 us kernel is not
+    host-bound)."""
     import torch
     from tilec_amd import ext
+    mm = mm or ext.matrix_mul
     nbuf = len(x2s)
     for i in range(nbuf):  # warm up: workspace exists before capture
-        ext.matrix_mul(x1, x2s[i])
+        mm(x1, x2s[i])
     torch.cuda.synchronize()
     reps = 4 * nbuf
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        ext.matrix_mul(x1, x2s[0])
+        mm(x1, x2s[0])
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=s):
-            outs = [ext.matrix_mul(x1, x2s[i % nbuf]) for i in range(reps)]
+            outs = [mm(x1, x2s[i % nbuf]) for i in range(reps)]
     torch.cuda.synchronize()
     replays = max(1, steps // reps)
     with torch.cuda.stream(s):
@@ -201,6 +206,54 @@ def bench_bf16(steps=10, warmup=2):
     tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
     log(f"bf16 8192^3: {ms:.3f} ms, {tflops:.1f} TFLOP/s ({cfg})")
     return dict(ms=ms, TFLOPs=tflops, frac=tflops / PEAK_BF16_MFMA, config=list(cfg))
+
+
+def _vendor_mm(a, b):
+    """torch's library product (hipBLASLt / rocBLAS) with an fp32 result, as
+    ext.matrix_mul returns: bf16 inputs use the out_dtype form of torch.mm."""
+    import torch
+    if a.dtype == torch.bfloat16:
+        return torch.mm(a, b, out_dtype=torch.float32)
+    return torch.mm(a, b)
+
+
+def bench_vendor(steps=200):
+    """The same cases through torch.mm (ROCm's hipBLASLt / rocBLAS) on the
+    same box, data and timing protocol: the square fp32 GEMM, config 4 bf16
+    and the GEMVs.  A reference point for what the vendor library reaches
+    here, not part of the product."""
+    import torch
+    from oracle import oracle as O
+    out = {}
+    n = 4096
+    a = torch.from_numpy(O.uniform((n, n), 4)).cuda()
+    b = torch.from_numpy(O.uniform((n, n), 5)).cuda()
+    ms = timed(lambda: _vendor_mm(a, b), 20, 3)
+    out["f32_4096"] = dict(ms=ms, TFLOPs=2 * n ** 3 / (ms * 1e-3) / 1e12)
+    del a, b
+    n = 8192
+    sigma = n ** -0.25
+    a = torch.from_numpy(O.normal((n, n), 8, std=sigma)).to(torch.bfloat16).cuda()
+    b = torch.from_numpy(O.normal((n, n), 9, std=sigma)).to(torch.bfloat16).cuda()
+    ms = timed(lambda: _vendor_mm(a, b), 10, 2)
+    out["bf16_8192"] = dict(ms=ms, TFLOPs=2 * n ** 3 / (ms * 1e-3) / 1e12)
+    del a, b
+    K = N = 4096
+    for dtype, Ms in (("f32", (1, 16)), ("bf16", (1, 16))):
+        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+        esz = 4 if dtype == "f32" else 2
+        nbuf = (512 << 20) // (esz * K * N)
+        x2s = [torch.from_numpy(O.normal((K, N), 3 + 1000 * i)).to(tdt).cuda() for i in range(nbuf)]
+        for M in Ms:
+            x1 = torch.from_numpy(O.normal((M, K), 2)).to(tdt).cuda()
+            us = _gemv(x1, x2s, steps, mm=_vendor_mm)
+            nbytes = esz * (M * K + K * N) + 4 * M * N
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out[f"gemv_{dtype}_M{M}"] = dict(us=us, GBps=gbs, frac=gbs / PEAK_HBM)
+        del x2s
+    for k, v in out.items():
+        log(f"torch.mm {k}: " + ", ".join(f"{f}={x:.3f}" for f, x in v.items()))
+    return out
 
 
 CONFIG_CASES = (
@@ -384,7 +437,7 @@ def main():
     if args.only:
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
                "configs": bench_configs, "layouts": bench_layouts, "reduce": bench_reduce,
-               "copy": bench_copy}[args.only]()
+               "vendor": bench_vendor, "copy": bench_copy}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return
 
@@ -396,6 +449,7 @@ def main():
         extra["configs"] = bench_configs()
         extra["layouts"] = bench_layouts()
         extra["reduce"] = bench_reduce()
+        extra["vendor_torch_mm"] = bench_vendor()
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
 
     rec = {

@@ -13,8 +13,10 @@
 //     other's barrier and load waits);
 //   * A and B tiles double-buffered in LDS with one barrier per K step; the
 //     next tile's global loads are issued before the current tile's MFMAs;
-//   * A stored k-major in LDS (As[k][m]) so every MFMA operand read is one
-//     conflict-free 32-bit LDS read per lane for both operands;
+//   * tiles kept in LDS as loaded (16-byte stores): a k-contiguous operand
+//     gives each lane the 4 consecutive k of four MFMAs in one 16-byte read
+//     (the MFMAs of an 8-deep k chunk take k = 8c + 4h + e in lane half h),
+//     the other kind one 4-byte read per MFMA, both free of bank conflicts;
 //   * branch-free edges, as the reference's if-converted masked loads
 //     (README.md:50): with row strides that fit 32-bit offsets (BUF), every
 //     tile loads through buffer resources that end at the matrix's last
@@ -37,8 +39,14 @@ struct GemmF32 {
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-  static_assert(BK % 4 == 0 && BK % 2 == 0, "BK");
-  static constexpr size_t kLds = sizeof(float) * 2 * BK * ((BM + 4) + (BN + 4));
+  static_assert(BK % 8 == 0, "BK: whole 8-deep k chunks");
+  // K chunk (8 deep: four MFMA k-pairs) after whose MFMAs the next tile goes
+  // from registers to LDS.  With enough MFMAs per step the store sits
+  // mid-step, where its LDS writes overlap the matrix cores and the step's
+  // global loads have long arrived; short steps store at the end, after the
+  // MFMAs have covered the loads.
+  static constexpr int KS = BK / 8;
+  static constexpr int kStoreAt = TM * TN * BK / 2 >= 96 ? KS / 2 : KS;
 };
 
 // Four consecutive floats at a 4-byte aligned address: one dwordx4 load,
@@ -75,12 +83,21 @@ __device__ __forceinline__ uint32_t extent(int64_t rows_left, int64_t ld, int64_
 // operand's element (r, k) is X[r * ld + k] (k contiguous: row-major x1,
 // column-major x2); otherwise X[k * ld + r] (r contiguous: row-major x2,
 // column-major x1).  Each thread moves Q quads of 4 elements contiguous in
-// memory.  In LDS the tile is S[k][r] with rows of R + 4 floats, the layout
-// the MFMA operand reads expect for either operand.
+// memory.
+//
+// LDS layout, as loaded (16-byte stores, no transposition):
+//   KC: S[r][k], rows of LK = BK + 4 floats.  An MFMA operand fragment is one
+//     16-byte read of 4 consecutive k; lanes 0-7 read rows r..r+7 of one
+//     chunk, 9 (or 5) chunks apart mod 16: no bank conflicts.
+//   RC: S[k][r], rows of LR = R + 8 floats.  An operand is one 4-byte read
+//     per MFMA: 32 consecutive r per half wave at rows k and k + 4, whose
+//     4 * LR = 32 mod 64 banks apart: the halves use disjoint banks.
 template <int R, int BK, int NT, bool KC, bool VEC, bool BUF>
 struct OperandF32 {
   static constexpr int Q = R * BK / 4 / NT;
-  static constexpr int LDS_S = R + 4;
+  static constexpr int LK = BK + 4, LR = R + 8;
+  static constexpr int STAGE = KC ? R * LK : BK * LR;  // floats per LDS stage
+  static_assert(R % 32 == 0 && BK % 8 == 0, "tile shape");
   static_assert(R * BK % (4 * NT) == 0, "tile loads must divide evenly");
   const float* X;
   int64_t ld;
@@ -160,13 +177,19 @@ struct OperandF32 {
 
   __device__ __forceinline__ void store(float* __restrict__ S) const {
 #pragma unroll
-    for (int p = 0; p < Q; ++p) {
-      if constexpr (KC) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) S[(tk[p] + c) * LDS_S + tr[p]] = v[p][c];
-      } else {
-        *reinterpret_cast<f32x4*>(S + tk[p] * LDS_S + tr[p]) = v[p];
-      }
+    for (int p = 0; p < Q; ++p)
+      *reinterpret_cast<f32x4*>(S + (KC ? tr[p] * LK + tk[p] : tk[p] * LR + tr[p])) = v[p];
+  }
+
+  // Operand values of rows r0 + lane % 32 for the four MFMAs of k chunk c
+  // (k = 8c .. 8c + 7): MFMA e takes k = 8c + 4h + e in lane half h, so a
+  // KC fragment is the lane's 4 consecutive k in one read.
+  __device__ __forceinline__ static f32x4 frag(const float* __restrict__ S, int r, int c, int h) {
+    if constexpr (KC) {
+      return *reinterpret_cast<const f32x4*>(S + r * LK + 8 * c + 4 * h);
+    } else {
+      const float* p = S + (8 * c + 4 * h) * LR + r;
+      return f32x4{p[0], p[LR], p[2 * LR], p[3 * LR]};
     }
   }
 };
@@ -183,8 +206,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
   using OpB = OperandF32<BN, BK, P::NT, CB, VEC, BUF>;
   extern __shared__ __align__(16) float lds[];
   __shared__ int last_flag;
-  float* As = lds;                          // [2][BK][BM + 4]
-  float* Bs = lds + 2 * BK * OpA::LDS_S;    // [2][BK][BN + 4]
+  float* As = lds;                   // 2 stages of OpA::STAGE floats
+  float* Bs = lds + 2 * OpA::STAGE;  // 2 stages of OpB::STAGE floats
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -209,8 +232,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
     opb.load(kt, mask);
   };
   auto sstore = [&](int buf) {
-    opa.store(As + buf * BK * OpA::LDS_S);
-    opb.store(Bs + buf * BK * OpB::LDS_S);
+    opa.store(As + buf * OpA::STAGE);
+    opb.store(Bs + buf * OpB::STAGE);
   };
 
   f32x16 acc[P::TM][P::TN];
@@ -231,26 +254,33 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
   const int bcol = wn * P::WTN + (lane & 31);
   const int khalf = lane >> 5;
 
+  // The other LDS buffer was last read in the previous step, which ended
+  // with a barrier, so the next tile can be stored into it at any point of
+  // this step.  On the last step nothing was loaded and the store rewrites
+  // the registers' previous tile into a buffer no one reads again; storing
+  // unconditionally keeps the step one basic block.
   for (int kt = kt0; kt < kt1; ++kt) {
     const int buf = (kt - kt0) & 1;
     const bool more = kt + 1 < kt1;
     if (more) gload(kt + 1, !(interior && kt + 1 < nk_full));
-    const float* as = As + buf * BK * OpA::LDS_S;
-    const float* bs = Bs + buf * BK * OpB::LDS_S;
+    const float* as = As + buf * OpA::STAGE;
+    const float* bs = Bs + buf * OpB::STAGE;
 #pragma unroll
-    for (int ks = 0; ks < BK / 2; ++ks) {
-      const int k = 2 * ks + khalf;
-      float a[P::TM], b[P::TN];
+    for (int c = 0; c < P::KS; ++c) {
+      if (c == P::kStoreAt) sstore(buf ^ 1);
+      f32x4 a[P::TM], b[P::TN];
 #pragma unroll
-      for (int i = 0; i < P::TM; ++i) a[i] = as[k * OpA::LDS_S + arow + 32 * i];
+      for (int i = 0; i < P::TM; ++i) a[i] = OpA::frag(as, arow + 32 * i, c, khalf);
 #pragma unroll
-      for (int j = 0; j < P::TN; ++j) b[j] = bs[k * OpB::LDS_S + bcol + 32 * j];
+      for (int j = 0; j < P::TN; ++j) b[j] = OpB::frag(bs, bcol + 32 * j, c, khalf);
 #pragma unroll
-      for (int i = 0; i < P::TM; ++i)
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int j = 0; j < P::TN; ++j) acc[i][j] = mfma32x32x2(a[i], b[j], acc[i][j]);
+        for (int i = 0; i < P::TM; ++i)
+#pragma unroll
+          for (int j = 0; j < P::TN; ++j) acc[i][j] = mfma32x32x2(a[i][e], b[j][e], acc[i][j]);
     }
-    if (more) sstore(buf ^ 1);
+    if (P::kStoreAt == P::KS) sstore(buf ^ 1);
     __syncthreads();
   }
 
@@ -280,7 +310,8 @@ hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
   const SplitGeom g = gemm_split_geom(a.K, BK, a.split_k);
   if (g.splits > 1 && P::TM * P::TN * 16 > kSplitMaxAccPerThread) return hipErrorInvalidConfiguration;
   grid.y = (unsigned)g.splits;
-  const size_t lds = P::kLds;
+  const size_t lds = sizeof(float) * 2 *
+                     (OperandF32<BM, BK, P::NT, !CA, VEC, BUF>::STAGE + OperandF32<BN, BK, P::NT, CB, VEC, BUF>::STAGE);
   static std::atomic<uint64_t> lds_devices{0};
   const hipError_t e = raise_lds_limit((const void*)k, lds, lds_devices);
   if (e != hipSuccess) return e;
