@@ -45,6 +45,10 @@ struct GemmF32 {
   // mid-step, where its LDS writes overlap the matrix cores and the step's
   // global loads have long arrived; short steps store at the end, after the
   // MFMAs have covered the loads.
+  // Waves per SIMD the register budget is held to: 4-wave workgroups with
+  // at most 128 accumulators per lane fit two workgroups per CU, whose
+  // barriers are independent, so one's MFMAs cover the other's waits.
+  static constexpr int kWavesPerSimd = (WM * WN == 4 && TM * TN * 16 <= 128) ? 2 : 1;
   static constexpr int KS = BK / 8;
   static constexpr int kStoreAt = TM * TN * BK / 2 >= 96 ? KS / 2 : KS;
 };
@@ -197,7 +201,7 @@ struct OperandF32 {
 // CA: x1 is column-major (element (m, k) at A[m + k * lda]); CB: x2 is
 // column-major (element (k, n) at B[k + n * ldb]).
 template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF, bool CA, bool CB>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(
+__global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesPerSimd)) void gemm_f32_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
     unsigned* __restrict__ counters) {
@@ -378,6 +382,8 @@ const VariantDesc* gemm_f32_variants(int* count) {
        launch_gemm_f32<128, 128, 16, 2, 4>},
       {"gemm_f32_128x128x32_w2x4", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 32, 8, 0, 1,
        launch_gemm_f32<128, 128, 32, 2, 4>},
+      {"gemm_f32_128x128x32_w2x2", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 32, 4, 0, 1,
+       launch_gemm_f32<128, 128, 32, 2, 2>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;
