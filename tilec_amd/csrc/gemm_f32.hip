@@ -26,6 +26,8 @@
 //     edge tiles cost what interior ones do; otherwise clamped addresses plus
 //     selects on edge tiles and the K tail;
 //   * XCD-aware, grouped tile order (tile_of in common.h).
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/tilec.h"
 
@@ -108,7 +110,7 @@ struct OperandF32 {
   int r0, Rtot, K;
   int tr[Q], tk[Q], rvalid[Q];
   uint32_t off[Q];
-  f32x4 v[Q];
+  f32x4 v[2][Q];  // two register sets: one tile waits for its LDS store while the next loads
 
   // Tile row and tile k of the first element of quad e.
   __device__ __forceinline__ static void coord(int e, int& r, int& k) {
@@ -149,6 +151,7 @@ struct OperandF32 {
   // !VEC) a select that clears the columns past the edge inside the quad that
   // straddles it.  Otherwise MASK selects clamped, per-element loads at
   // every edge and unmasked 16-byte loads elsewhere.
+  template <int SET>
   __device__ __forceinline__ void load(int kt, bool mask) {
     const int k0 = kt * BK;
     if constexpr (BUF) {
@@ -162,7 +165,7 @@ struct OperandF32 {
 #pragma unroll
           for (int c = 1; c < 4; ++c) x[c] = c < valid ? x[c] : 0.f;
         }
-        v[p] = x;
+        v[SET][p] = x;
       }
       return;
     }
@@ -171,18 +174,19 @@ struct OperandF32 {
       const int gr = r0 + tr[p], gk = k0 + tk[p];
       const int64_t at = KC ? (int64_t)gr * ld + gk : (int64_t)gk * ld + gr;
       if (!mask) {  // whole quad in bounds: one (dword-aligned) 16-byte load
-        v[p] = *reinterpret_cast<const f32x4_a4*>(X + at);
+        v[SET][p] = *reinterpret_cast<const f32x4_a4*>(X + at);
       } else {
         const int valid = KC ? (gr < Rtot ? max(0, min(4, K - gk)) : 0) : (gk < K ? max(0, min(4, Rtot - gr)) : 0);
-        v[p] = ld4<VEC>(X + (valid > 0 ? at : 0), valid == 4, valid);
+        v[SET][p] = ld4<VEC>(X + (valid > 0 ? at : 0), valid == 4, valid);
       }
     }
   }
 
+  template <int SET>
   __device__ __forceinline__ void store(float* __restrict__ S) const {
 #pragma unroll
     for (int p = 0; p < Q; ++p)
-      *reinterpret_cast<f32x4*>(S + (KC ? tr[p] * LK + tk[p] : tk[p] * LR + tr[p])) = v[p];
+      *reinterpret_cast<f32x4*>(S + (KC ? tr[p] * LK + tk[p] : tk[p] * LR + tr[p])) = v[SET][p];
   }
 
   // Operand values of rows r0 + lane % 32 for the four MFMAs of k chunk c
@@ -231,14 +235,19 @@ __global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesP
   OpB opb;
   opa.init(A, lda, m0, M, K, tid);
   opb.init(B, ldb, n0, N, K, tid);
-  auto gload = [&](int kt, bool mask) {
-    opa.load(kt, mask);
-    opb.load(kt, mask);
+  // Tile t (counted from kt0) moves through register set t % 2 and LDS
+  // buffer t % 2.
+  auto gload = [&](auto set, int kt, bool mask) {
+    opa.template load<decltype(set)::value>(kt, mask);
+    opb.template load<decltype(set)::value>(kt, mask);
   };
-  auto sstore = [&](int buf) {
-    opa.store(As + buf * OpA::STAGE);
-    opb.store(Bs + buf * OpB::STAGE);
+  auto sstore = [&](auto set) {
+    constexpr int T = decltype(set)::value;
+    opa.template store<T>(As + T * OpA::STAGE);
+    opb.template store<T>(Bs + T * OpB::STAGE);
   };
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
 
   f32x16 acc[P::TM][P::TN];
 #pragma unroll
@@ -249,8 +258,9 @@ __global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesP
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   if (kt0 < kt1) {
-    gload(kt0, !(interior && kt0 < nk_full));
-    sstore(0);
+    gload(Set0{}, kt0, !(interior && kt0 < nk_full));
+    if (kt0 + 1 < kt1) gload(Set1{}, kt0 + 1, !(interior && kt0 + 1 < nk_full));
+    sstore(Set0{});
     __syncthreads();
   }
 
@@ -258,20 +268,22 @@ __global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesP
   const int bcol = wn * P::WTN + (lane & 31);
   const int khalf = lane >> 5;
 
-  // The other LDS buffer was last read in the previous step, which ended
-  // with a barrier, so the next tile can be stored into it at any point of
-  // this step.  On the last step nothing was loaded and the store rewrites
-  // the registers' previous tile into a buffer no one reads again; storing
+  // Step t computes from LDS buffer t % 2 and stores tile t + 1 (loaded one
+  // step earlier into set (t + 1) % 2) into the other buffer, which was last
+  // read in step t - 1, before that step's barrier; it issues the loads of
+  // tile t + 2 into set t % 2, whose tile went to LDS in step t - 1.  A load
+  // thus has one to two steps to arrive.  Past the last tile the store
+  // rewrites stale registers into a buffer no one reads again; storing
   // unconditionally keeps the step one basic block.
-  for (int kt = kt0; kt < kt1; ++kt) {
-    const int buf = (kt - kt0) & 1;
-    const bool more = kt + 1 < kt1;
-    if (more) gload(kt + 1, !(interior && kt + 1 < nk_full));
-    const float* as = As + buf * OpA::STAGE;
-    const float* bs = Bs + buf * OpB::STAGE;
+  auto step = [&](int kt, auto par) __attribute__((always_inline)) {
+    constexpr int T = decltype(par)::value;
+    using Next = std::integral_constant<int, T ^ 1>;
+    if (kt + 2 < kt1) gload(par, kt + 2, !(interior && kt + 2 < nk_full));
+    const float* as = As + T * OpA::STAGE;
+    const float* bs = Bs + T * OpB::STAGE;
 #pragma unroll
     for (int c = 0; c < P::KS; ++c) {
-      if (c == P::kStoreAt) sstore(buf ^ 1);
+      if (c == P::kStoreAt) sstore(Next{});
       f32x4 a[P::TM], b[P::TN];
 #pragma unroll
       for (int i = 0; i < P::TM; ++i) a[i] = OpA::frag(as, arow + 32 * i, c, khalf);
@@ -284,9 +296,15 @@ __global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesP
 #pragma unroll
           for (int j = 0; j < P::TN; ++j) acc[i][j] = mfma32x32x2(a[i][e], b[j][e], acc[i][j]);
     }
-    if (P::kStoreAt == P::KS) sstore(buf ^ 1);
+    if (P::kStoreAt == P::KS) sstore(Next{});
     __syncthreads();
+  };
+  int kt = kt0;
+  for (; kt + 1 < kt1; kt += 2) {
+    step(kt, Set0{});
+    step(kt + 1, Set1{});
   }
+  if (kt < kt1) step(kt, Set0{});
 
   // Epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each block.
   const int row_base = m0 + wm * P::WTM + 4 * khalf;
