@@ -126,8 +126,9 @@ def test_gemm_split_geometry_matches_the_library():
 
 def test_tune_features_and_shapes():
     f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8)
-    assert len(f) == 18 and all(math.isfinite(x) for x in f) and f[-2:] == [0.0, 0.0]
-    assert tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8, layout=3)[-2:] == [1.0, 1.0]
+    assert len(f) == 19 and all(math.isfinite(x) for x in f) and f[-3:-1] == [0.0, 0.0]
+    assert tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8, layout=3)[-3:-1] == [1.0, 1.0]
+    assert tune.features(1, 4096, 4096, 256, "f32", "skinny_f32_v1_w4_b2", 4)[-1] == 1.0
     s = tune.shapes(120, seed=0, n_layout=40)
     assert s == tune.shapes(120, seed=0, n_layout=40)
     rm = [x for x in s if x[4] == 0]

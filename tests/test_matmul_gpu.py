@@ -113,7 +113,10 @@ def test_f32_variant_ragged(name):
 
 @pytest.mark.parametrize("name", bf16_variants())
 def test_bf16_variant_ragged(name):
+    v = _lib.variants()[_lib.variant_id(name)]
     for i, (m, k, n) in enumerate(RAGGED):
+        if v["max_m"] and m > v["max_m"]:
+            continue
         a16 = O.bf16_round(O.normal((m, k), 300 + 2 * i))
         b16 = O.bf16_round(O.normal((k, n), 301 + 2 * i))
         say(f"{name} shape {(m, k, n)}")
@@ -195,6 +198,40 @@ def test_skinny_bf16():
     want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
     for cfg in [("skinny_bf16_w4_b1", 1), ("skinny_bf16_w8_b2", 8), ("skinny_bf16_w4_b2", 3)]:
         np.testing.assert_array_equal(run(dev(a).to(torch.bfloat16), dev(b).to(torch.bfloat16), cfg), want)
+
+
+def test_skinny_fma_path():
+    """The FMA variants (M <= 1 or 4, row-major x2; a column-major x2 runs the
+    MFMA path): every M up to the variant's bound, ragged and aligned K and
+    N, row- and column-major x1, split K, against the fp64 oracle; small
+    integers bit-exact."""
+    fma = [v for v in _lib.variants() if v["family"] == _lib.FAMILY_SKINNY and v["max_m"]]
+    assert len(fma) == 8
+    for v in fma:
+        bf = v["dtype"] == _lib.BF16
+        for m in range(1, v["max_m"] + 1):
+            for i, (k, n) in enumerate([(1, 1), (5, 63), (1000, 65), (4096, 136), (4097, 130), (333, 1000)]):
+                a, b = O.normal((m, k), 40 * m + i), O.normal((k, n), 40 * m + i + 20)
+                if bf:
+                    a, b = O.bf16_round(a), O.bf16_round(b)
+                ref = O.matmul_bf16_f64(a, b) if bf else O.matmul_f64(a, b)
+                mk = dev_bf16 if bf else dev
+                for layout in (0, _lib.X1_COL_MAJOR, _lib.X2_COL_MAJOR):
+                    for s in (1, 3, 8):
+                        say(f"{v['name']} m={m} k={k} n={n} layout {layout} split {s}")
+                        got = run_layout(mk(a), mk(b), layout, (v["name"], s))
+                        assert O.rel_l2(got, ref) <= (1e-5 if bf else O.TOL_F32), (v["name"], m, k, n, layout, s)
+    rng = np.random.default_rng(21)
+    for m in (1, 3, 4):
+        a = rng.integers(-3, 4, (m, 3001)).astype(np.float32)
+        b = rng.integers(-3, 4, (3001, 260)).astype(np.float32)
+        want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+        for v in fma:
+            if m > v["max_m"]:
+                continue
+            conv = (lambda x: dev(x).to(torch.bfloat16)) if v["dtype"] == _lib.BF16 else dev
+            for s in (1, 5):
+                np.testing.assert_array_equal(run(conv(a), conv(b), (v["name"], s)), want)
 
 
 def test_skinny_row_blocks():
@@ -403,6 +440,8 @@ def test_f32_variant_layouts(name):
     v = _lib.variants()[_lib.variant_id(name)]
     for layout in LAYOUTS:
         for i, (m, k, n) in enumerate(LAYOUT_SHAPES):
+            if v["max_m"] and m > v["max_m"]:
+                continue
             a, b = O.normal((m, k), 500 + 2 * i), O.normal((k, n), 501 + 2 * i)
             ref = O.matmul_f64(a, b)
             splits = [1] if v["family"] == _lib.FAMILY_GEMM else [1, 3, 8]
@@ -417,6 +456,8 @@ def test_bf16_variant_layouts(name):
     v = _lib.variants()[_lib.variant_id(name)]
     for layout in LAYOUTS:
         for i, (m, k, n) in enumerate(LAYOUT_SHAPES):
+            if v["max_m"] and m > v["max_m"]:
+                continue
             a16 = O.bf16_round(O.normal((m, k), 600 + 2 * i))
             b16 = O.bf16_round(O.normal((k, n), 601 + 2 * i))
             ref = O.matmul_bf16_f64(a16, b16)

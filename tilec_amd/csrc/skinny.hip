@@ -49,6 +49,8 @@
 // block, slab) to finish (completion counter) adds the partials in split
 // order, so results do not depend on scheduling; it resets the counter to
 // zero.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/tilec.h"
 
@@ -113,6 +115,23 @@ struct Blk<u16, true> {
   i32x4 a;
 };
 
+// FMA path (MV > 0, row-major x2 only): the same x2 block and, for each of
+// the MV output rows m, x1[m][4r .. 4r+3] (every lane needs every row).
+template <typename T, int MV>
+struct BlkV;
+template <int MV>
+struct BlkV<float, MV> {
+  static constexpr int KB = 16;
+  f32x4 b[4];
+  f32x4 a[MV];
+};
+template <int MV>
+struct BlkV<u16, MV> {
+  static constexpr int KB = 16;
+  i32x4 b[4];
+  i32x2 a[MV];
+};
+
 __device__ __forceinline__ float bf16_lo(int w) { return __int_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(int w) { return __int_as_float(w & (int)0xffff0000u); }
 
@@ -149,13 +168,20 @@ __device__ __forceinline__ void store_quad(float* __restrict__ row, int col, int
   }
 }
 
-template <typename T, int WAVES, int UB, bool VEC, bool CA, bool CB>
+// MV = 0: MFMA path (any M <= 16 per row block).  MV in 1..4: FMA path for
+// M <= MV with row-major x2 — lane (r, q) accumulates out[m][col + c] over
+// its own rows 4r + u of each block in plain FMAs, and the four lanes of a
+// column group (r = 0..3) meet in the LDS reduction as four more "waves".
+// Per 4 KiB of x2 a wave then spends 16 MV FMAs (fp32) where the MFMA path
+// issues 16 MFMAs of 8 passes, and bf16 needs no widening to 32 MFMAs.
+template <typename T, int WAVES, int UB, bool VEC, bool CA, bool CB, int MV>
 __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
     const T* __restrict__ x1, const T* __restrict__ x2, float* __restrict__ out,
     int M_all, int N, int K, int64_t ldx1, int64_t ldx2, int64_t ldo, int kc,
     unsigned* __restrict__ counters, float* __restrict__ part) {
+  static_assert(MV >= 0 && MV <= 4 && (MV == 0 || !CB), "FMA path: M <= 4, row-major x2");
   using E = Elem<T>;
-  using Block = Blk<T, CB>;
+  using Block = std::conditional_t<(MV > 0), BlkV<T, (MV > 0 ? MV : 1)>, Blk<T, CB>>;
   constexpr int CPL = E::CPL, NQ = CPL / 4, SLAB = kSlabOf<T>, NT = WAVES * 64;
   constexpr int EPL = 16 / E::BYTES;  // elements per 16-byte load
   constexpr int KB = Block::KB;       // rows of K per block
@@ -229,8 +255,30 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
           put(blk.b[u], h);
         }
       }
-      // x1[q][4r .. 4r+3]
-      if constexpr (VEC && !CA) {  // K % 4 == 0: the 4 k of a lane are all valid or all past the chunk
+      if constexpr (MV > 0) {
+        // x1[m][4r .. 4r+3] for every row m < MV: 0 past M or past the chunk
+#pragma unroll
+        for (int m = 0; m < (MV > 0 ? MV : 1); ++m) {
+          auto off = [&](int kr) -> uint32_t {
+            if (!((m < M) & (brow + kr < nrows))) return kOob;
+            return CA ? EB * ((uint32_t)kr * (uint32_t)ldx1 + (uint32_t)m) : EB * ((uint32_t)m * (uint32_t)ldx1 + (uint32_t)kr);
+          };
+          if constexpr (VEC && !CA) {
+            if constexpr (CPL == 4) blk.a[m] = load_f32x4(rx1, off(4 * r));
+            else blk.a[m] = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(rx1, (int)off(4 * r), 0, 0));
+          } else {
+            int h[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) h[u] = ld_elem(rx1, off(4 * r + u));
+            if constexpr (CPL == 4) {
+              put(blk.a[m], h);
+            } else {
+              blk.a[m][0] = h[0] | (h[1] << 16);
+              blk.a[m][1] = h[2] | (h[3] << 16);
+            }
+          }
+        }
+      } else if constexpr (VEC && !CA) {  // x1[q][4r .. 4r+3]; K % 4 == 0: the 4 k of a lane are all valid or all past the chunk
         const uint32_t o = x1_off(brow, 4 * r);
         if constexpr (CPL == 4) blk.a = load_f32x4(rx1, o);
         else blk.a = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(rx1, (int)o, 0, 0));
@@ -279,8 +327,30 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
   f32x4 acc[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  constexpr int MVA = MV > 0 ? MV : 1;
+  f32x4 accv[MVA][NQ];  // FMA path: out[m][col + 4h .. +3] over this lane's rows
+#pragma unroll
+  for (int m = 0; m < MVA; ++m)
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) accv[m][h] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto mma_block = [&](const Block& blk) __attribute__((always_inline)) {
-    if constexpr (!CB) {
+    if constexpr (MV > 0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int m = 0; m < MVA; ++m) {
+          float a;
+          if constexpr (CPL == 4) a = blk.a[m][u];
+          else a = (u & 1) ? bf16_hi(blk.a[m][u >> 1]) : bf16_lo(blk.a[m][u >> 1]);
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc) {
+            float b;
+            if constexpr (CPL == 4) b = blk.b[u][cc];
+            else b = (cc & 1) ? bf16_hi(blk.b[u][cc >> 1]) : bf16_lo(blk.b[u][cc >> 1]);
+            accv[m][cc / 4][cc % 4] = __builtin_fmaf(a, b, accv[m][cc / 4][cc % 4]);
+          }
+        }
+    } else if constexpr (!CB) {
       // D_c[m][q] += sum_r x1[m][4r+u] * x2[4r+u][col + c]
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -344,7 +414,16 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
   }
 
   // Item (row m, column group q, half h) holds out[m][n0 + CPL*q + 4h .. +3].
-  if constexpr (!CB) {
+  // The FMA path has kRows = MV rows and kVW = 4 WAVES partials per item
+  // (lane rows r = 0..3 of every wave).
+  constexpr int kRows = MV > 0 ? MV : kMaxM;
+  constexpr int kVW = MV > 0 ? 4 * WAVES : WAVES;
+  if constexpr (MV > 0) {
+#pragma unroll
+    for (int m = 0; m < MVA; ++m)
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) red[(((wave * 4 + r) * kRows + m) * 16 + q) * NQ + h] = accv[m][h];
+  } else if constexpr (!CB) {
     // Lane l holds D_c[4r + v][q] in acc[c][v]: out row 4r+v, column col + c.
 #pragma unroll
     for (int v = 0; v < 4; ++v)
@@ -364,11 +443,12 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
 
   // Output items: (row m, column group q, half h) -> 4 columns at
   // SLAB*slab + CPL*q + 4h; 256*NQ of them, spread over the workgroup.
-  constexpr int kItems = kMaxM * 16 * NQ;
+  constexpr int kItems = kRows * 16 * NQ;
+  static_assert(kVW * kItems <= WAVES * kMaxM * 16 * NQ, "red holds every partial");
   auto item_sum = [&](int it) {
     f32x4 v = red[it];
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) v += red[w * kItems + it];
+    for (int w = 1; w < kVW; ++w) v += red[w * kItems + it];
     return v;
   };
   auto item_col = [&](int it) { return slab * SLAB + CPL * ((it / NQ) % 16) + 4 * (it % NQ); };
@@ -444,15 +524,15 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
   }
 }
 
-template <typename T, int WAVES, int UB, bool VEC, bool CA, bool CB>
+template <typename T, int WAVES, int UB, bool VEC, bool CA, bool CB, int MV>
 hipError_t launch_one(const MatmulArgs& a, const SkinnyGeom& g, unsigned* counters, float* part) {
-  hipLaunchKernelGGL((skinny_kernel<T, WAVES, UB, VEC, CA, CB>), dim3((unsigned)g.nslabs, (unsigned)g.splits, (unsigned)g.nrb),
+  hipLaunchKernelGGL((skinny_kernel<T, WAVES, UB, VEC, CA, CB, MV>), dim3((unsigned)g.nslabs, (unsigned)g.splits, (unsigned)g.nrb),
                      dim3(WAVES * 64), 0, a.stream, static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out,
                      (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo, (int)g.kc, counters, part);
   return hipGetLastError();
 }
 
-template <typename T, int WAVES, int UB, bool CA, bool CB>
+template <typename T, int WAVES, int UB, bool CA, bool CB, int MV>
 hipError_t launch_layout(const MatmulArgs& a, const SkinnyGeom& g, unsigned* counters, float* part) {
   constexpr int CPL = Elem<T>::CPL, EPL = 16 / (int)sizeof(T);
   auto aligned = [](const void* p, size_t n) { return reinterpret_cast<uintptr_t>(p) % n == 0; };
@@ -466,20 +546,22 @@ hipError_t launch_layout(const MatmulArgs& a, const SkinnyGeom& g, unsigned* cou
   else
     vec = vec && a.N % 4 == 0 && a.K % EPL == 0 && a.ldx2 % EPL == 0 &&
           (CA || (a.ldx1 % EPL == 0 && aligned(a.x1, 16)));
-  return vec ? launch_one<T, WAVES, UB, true, CA, CB>(a, g, counters, part)
-             : launch_one<T, WAVES, UB, false, CA, CB>(a, g, counters, part);
+  // The FMA path takes row-major x2; a column-major x2 runs the MFMA path.
+  constexpr int MVL = CB ? 0 : MV;
+  return vec ? launch_one<T, WAVES, UB, true, CA, CB, MVL>(a, g, counters, part)
+             : launch_one<T, WAVES, UB, false, CA, CB, MVL>(a, g, counters, part);
 }
 
-template <typename T, int WAVES, int UB>
+template <typename T, int WAVES, int UB, int MV = 0>
 hipError_t launch_skinny(const MatmulArgs& a) {
   const SkinnyGeom g = skinny_geom(a.M, a.N, a.K, a.split_k, kSlabOf<T>);
   unsigned* counters = g.splits > 1 ? a.counters : nullptr;
   float* part = g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr;
   switch (a.layout & 3) {
-    case 0: return launch_layout<T, WAVES, UB, false, false>(a, g, counters, part);
-    case TILEC_X1_COL_MAJOR: return launch_layout<T, WAVES, UB, true, false>(a, g, counters, part);
-    case TILEC_X2_COL_MAJOR: return launch_layout<T, WAVES, UB, false, true>(a, g, counters, part);
-    default: return launch_layout<T, WAVES, UB, true, true>(a, g, counters, part);
+    case 0: return launch_layout<T, WAVES, UB, false, false, MV>(a, g, counters, part);
+    case TILEC_X1_COL_MAJOR: return launch_layout<T, WAVES, UB, true, false, MV>(a, g, counters, part);
+    case TILEC_X2_COL_MAJOR: return launch_layout<T, WAVES, UB, false, true, MV>(a, g, counters, part);
+    default: return launch_layout<T, WAVES, UB, true, true, MV>(a, g, counters, part);
   }
 }
 
@@ -499,6 +581,15 @@ const VariantDesc* skinny_variants(int* count) {
       {"skinny_bf16_w4_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 4, 0, 2, launch_skinny<u16, 4, 2>},
       {"skinny_bf16_w8_b1", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 8, 0, 1, launch_skinny<u16, 8, 1>},
       {"skinny_bf16_w8_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 8, 0, 2, launch_skinny<u16, 8, 2>},
+      // FMA path for M <= 1 and M <= 4 (row-major x2; column-major x2 runs the MFMA path).
+      {"skinny_f32_v1_w4_b2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlabOf<float>, kKcMax, 4, 1, 2, launch_skinny<float, 4, 2, 1>},
+      {"skinny_f32_v1_w8_b2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlabOf<float>, kKcMax, 8, 1, 2, launch_skinny<float, 8, 2, 1>},
+      {"skinny_f32_v4_w4_b2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlabOf<float>, kKcMax, 4, 4, 2, launch_skinny<float, 4, 2, 4>},
+      {"skinny_f32_v4_w8_b2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, kSlabOf<float>, kKcMax, 8, 4, 2, launch_skinny<float, 8, 2, 4>},
+      {"skinny_bf16_v1_w4_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 4, 1, 2, launch_skinny<u16, 4, 2, 1>},
+      {"skinny_bf16_v1_w8_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 8, 1, 2, launch_skinny<u16, 8, 2, 1>},
+      {"skinny_bf16_v4_w4_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 4, 4, 2, launch_skinny<u16, 4, 2, 4>},
+      {"skinny_bf16_v4_w8_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 8, 4, 2, launch_skinny<u16, 8, 2, 4>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

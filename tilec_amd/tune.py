@@ -58,7 +58,8 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
 
     Shape and config sizes enter as log2, plus the derived quantities that
     decide occupancy: workgroups launched per CU and the K rows per split,
-    and the operand layout bits (x1, x2 column-major).
+    the operand layout bits (x1, x2 column-major) and the variant's row
+    bound (max_m; 0 = any M), which tells the FMA streaming variants apart.
     """
     v = _variant_by_name()[kernel]
     tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
@@ -68,7 +69,8 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
             float(v["family"]), lg(v["bm"]), lg(v["bn"]), lg(v["bk"]), float(v["waves"]),
             float(v["unroll"]), lg(split_k), lg(tiles), math.log2(max(1, wgs) / cus),
             lg(cdiv(K, split_k)), lg(M * K * N),
-            float(layout & _lib.X1_COL_MAJOR != 0), float(layout & _lib.X2_COL_MAJOR != 0)]
+            float(layout & _lib.X1_COL_MAJOR != 0), float(layout & _lib.X2_COL_MAJOR != 0),
+            float(v["max_m"])]
 
 
 GRAPH_BELOW_MS = 0.2   # calls shorter than this are timed from a replayed HIP graph
@@ -435,7 +437,7 @@ def pick(M, K, N, dtype="f32", layout=0):
         return measured
     cus = _cus()
     if model.n_features < len(features(M, K, N, cus, dtype, cands[0][0], cands[0][1], layout)):
-        return None  # a model from before the layout features: use the built-in rule
+        return None  # a model trained on fewer features than these: use the built-in rule
     pred = model.predict([features(M, K, N, cus, dtype, k, s, layout) for k, s in cands])
     return cands[int(pred.argmin())]
 
