@@ -1,12 +1,13 @@
 """Benchmark of tilec.ext.matrix_mul on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-ms S] [--no-cpu] [--no-extra]
 
 Prints ONE JSON line.  The headline workload is BASELINE config 2 at its
 largest size, fp32 4096^3 (the metric's "TFLOP/s + %MFMA peak at 4096^3"):
 a step is one `matrix_mul` call on resident, seeded U(-1,1) inputs; K steps
-are timed between HIP events on the stream the kernel runs on, after W
-warmup steps.  Extra objects in the same line:
+are timed between HIP events on the stream the kernel runs on, after S ms of
+untimed calls (default 200: the GPU's clocks settle under sustained load)
+and W warmup steps.  Extra objects in the same line:
   roofline     — the 4096^3 kernel against the fp32 MFMA peak (157.3 TFLOP/s)
   skinny       — the metric's "GB/s + %HBM roofline at M<=16" (config 1):
                  M in {1,4,16} fp32 and {1,16} bf16, K=N=4096, x2 rotated
@@ -49,6 +50,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                   help="untimed calls before each GEMM timing, in ms of wall time (clock settling)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the skinny and bf16 sections")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
@@ -62,10 +65,32 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def timed(fn, steps, warmup, stream=None):
-    """Average ms per call of fn() over `steps` calls, between events recorded
-    on the stream the work is issued to."""
+# Untimed load before each GEMM timing.  After the GPU idles (process start,
+# data upload, a host pause), MI355X raises its clocks over the first 30-50 ms
+# of sustained matrix-core load: an 8192^3 bf16 product goes from 1.18 ms to
+# 0.87 ms over its first ~40 calls, a 4096^3 fp32 one from 1.16 to 0.98 ms.
+# Timing starts from the steady state a loop of products runs at.
+SETTLE_MS = 200.0
+
+
+def settle(fn, ms=SETTLE_MS, batch=4):
+    """Call fn() for `ms` of wall time, synchronizing every `batch` calls so
+    the queue never runs far ahead of the clock."""
     import torch
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(batch):
+            fn()
+        torch.cuda.synchronize()
+
+
+def timed(fn, steps, warmup, stream=None, settle_ms=0.0):
+    """Average ms per call of fn() over `steps` calls, between events recorded
+    on the stream the work is issued to, after `settle_ms` of untimed calls
+    (clock settling, see SETTLE_MS) and `warmup` more."""
+    import torch
+    if settle_ms > 0:
+        settle(fn, settle_ms)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -99,7 +124,7 @@ def bench_square(args):
     b = torch.from_numpy(O.uniform((n, n), 5)).cuda()
     cfg = kernel_name_for(n, n, n, "f32")
     log(f"square fp32 {n}^3 with {cfg}")
-    ms = timed(lambda: ext.matrix_mul(a, b), args.steps, args.warmup)
+    ms = timed(lambda: ext.matrix_mul(a, b), args.steps, args.warmup, settle_ms=args.settle_ms)
     tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
     return dict(ms=ms, tflops=tflops, config=cfg)
 
@@ -184,7 +209,7 @@ def bench_layouts(steps=200, gemm_steps=20):
         at, bt = a.t().contiguous().t(), b.t().contiguous().t()  # same values, column-major
         for name, x1, x2 in (("x1T", at, b), ("x2T", a, bt), ("x1T_x2T", at, bt)):
             cfg = kernel_name_for(n, n, n, dtype, ext.layout_of(x1, x2))
-            ms = timed(lambda: ext.matrix_mul(x1, x2), gemm_steps, 3)
+            ms = timed(lambda: ext.matrix_mul(x1, x2), gemm_steps, 3, settle_ms=SETTLE_MS)
             tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
             out[f"{dtype}_{n}_{name}"] = dict(ms=ms, TFLOPs=tflops, frac=tflops / peak, layout=ext.layout_of(x1, x2),
                                               config=list(cfg))
@@ -193,7 +218,7 @@ def bench_layouts(steps=200, gemm_steps=20):
     return out
 
 
-def bench_bf16(steps=10, warmup=2):
+def bench_bf16(steps=20, warmup=2):
     import torch
     from oracle import oracle as O
     from tilec_amd import ext
@@ -202,7 +227,7 @@ def bench_bf16(steps=10, warmup=2):
     a = torch.from_numpy(O.normal((n, n), 8, std=sigma)).to(torch.bfloat16).cuda()
     b = torch.from_numpy(O.normal((n, n), 9, std=sigma)).to(torch.bfloat16).cuda()
     cfg = kernel_name_for(n, n, n, "bf16")
-    ms = timed(lambda: ext.matrix_mul(a, b), steps, warmup)
+    ms = timed(lambda: ext.matrix_mul(a, b), steps, warmup, settle_ms=SETTLE_MS)
     tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
     log(f"bf16 8192^3: {ms:.3f} ms, {tflops:.1f} TFLOP/s ({cfg})")
     return dict(ms=ms, TFLOPs=tflops, frac=tflops / PEAK_BF16_MFMA, config=list(cfg))
@@ -228,14 +253,14 @@ def bench_vendor(steps=200):
     n = 4096
     a = torch.from_numpy(O.uniform((n, n), 4)).cuda()
     b = torch.from_numpy(O.uniform((n, n), 5)).cuda()
-    ms = timed(lambda: _vendor_mm(a, b), 20, 3)
+    ms = timed(lambda: _vendor_mm(a, b), 20, 3, settle_ms=SETTLE_MS)
     out["f32_4096"] = dict(ms=ms, TFLOPs=2 * n ** 3 / (ms * 1e-3) / 1e12)
     del a, b
     n = 8192
     sigma = n ** -0.25
     a = torch.from_numpy(O.normal((n, n), 8, std=sigma)).to(torch.bfloat16).cuda()
     b = torch.from_numpy(O.normal((n, n), 9, std=sigma)).to(torch.bfloat16).cuda()
-    ms = timed(lambda: _vendor_mm(a, b), 10, 2)
+    ms = timed(lambda: _vendor_mm(a, b), 20, 2, settle_ms=SETTLE_MS)
     out["bf16_8192"] = dict(ms=ms, TFLOPs=2 * n ** 3 / (ms * 1e-3) / 1e12)
     del a, b
     K = N = 4096
@@ -294,7 +319,7 @@ def bench_configs(reps=20):
                 outs = [ext.matrix_mul(x1, x2) for _ in range(reps)]
         torch.cuda.synchronize()
         with torch.cuda.stream(s):
-            ms = timed(g.replay, 3, 1, stream=s) / reps
+            ms = timed(g.replay, 3, 1, stream=s, settle_ms=SETTLE_MS / 2) / reps
         del outs
         tflops = 2 * M * N * K / (ms * 1e-3) / 1e12
         out[name] = dict(us=ms * 1e3, TFLOPs=tflops, frac=tflops / PEAK_FP32_MFMA, config=list(cfg))
@@ -459,6 +484,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": round(sq["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
