@@ -235,8 +235,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   // A fragment is 8 consecutive k of one of the wave's 32 rows (MFMA operand
   // layout: row lane % 32, k-half lane / 32).  From a k-contiguous stage it
   // is the 16-byte chunk 2 ks + h of that row; from an r-contiguous stage two
-  // transposing reads, of k-rows tr_krow (+4) and 8-row groups holding row
-  // rbase + 16 (g & 1) + 4 (jj & 3), return it.
+  // transposing reads, of k-rows 16 ks + tr_krow (+4) and 8-row groups
+  // holding row rbase + 16 (g & 1) + 4 (jj & 3), return it.
   const int h = lane >> 5;
   const int g = lane >> 4, jj = lane & 15;
   const int tr_row = 16 * (g & 1) + 4 * (jj & 3);
@@ -248,19 +248,43 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
 #pragma unroll
   for (int j = 0; j < P::TN; ++j) b_r[j] = wn * P::WTN + 32 * j + (CB ? (lane & 31) : tr_row);
 
-  auto frag = [&](auto st_t, const char* area, int r, int ks) __attribute__((always_inline)) -> bf16x8 {
+  // Transposing reads: the lane's byte offset from the stage base for k-slice
+  // 0 (for B including the A area), kept opaque so that every read's address
+  // is that one offset plus a constant (k-slice ks and second read add
+  // 16 * ROW_CHUNKS * (16 ks + 4)).  With shallow address chains the
+  // compiler's per-object LDS alias scopes reach every read, so the waits it
+  // places before LDS reads cover only the DMA copies into the same stage
+  // buffer; a read it cannot place waits for every DMA copy in flight,
+  // including the next step's.
+  uint32_t tr_a[P::TM], tr_b[P::TN];
+  auto tr_off = [&](auto st_t, int r) -> uint32_t {
+    using T = decltype(st_t);
+    return 16u * (uint32_t)(tr_krow * T::ROW_CHUNKS + ((r >> 3) ^ T::swz(tr_krow))) + 8u * (uint32_t)((r >> 2) & 1);
+  };
+#pragma unroll
+  for (int i = 0; i < P::TM; ++i) {
+    tr_a[i] = SA::kKC ? 0u : tr_off(SA{}, a_r[i]);
+    asm volatile("" : "+v"(tr_a[i]));
+  }
+#pragma unroll
+  for (int j = 0; j < P::TN; ++j) {
+    tr_b[j] = SB::kKC ? 0u : (uint32_t)P::A_BYTES + tr_off(SB{}, b_r[j]);
+    asm volatile("" : "+v"(tr_b[j]));
+  }
+
+  // kc stage: `area` is the operand's area, r its row.  r-contiguous stage:
+  // `area` is the stage base, `off` the lane's offset from tr_a / tr_b.
+  auto frag = [&](auto st_t, const char* area, int r, uint32_t off, int ks) __attribute__((always_inline)) -> bf16x8 {
     using T = decltype(st_t);
     if constexpr (T::kKC) {
       const int c = 2 * ks + h;
       return *reinterpret_cast<const bf16x8*>(area + 16 * (r * T::ROW_CHUNKS + (c ^ T::swz(r))));
     } else {
-      auto at = [&](int kr) {
-        return (__attribute__((address_space(3))) i16x4v*)(area + 16 * (kr * T::ROW_CHUNKS + ((r >> 3) ^ T::swz(kr))) +
-                                                          8 * ((r >> 2) & 1));
-      };
-      const int kr = 16 * ks + tr_krow;
-      const i16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(at(kr));
-      const i16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(at(kr + 4));
+      typedef __attribute__((address_space(3))) i16x4v lds_i16x4;
+      constexpr uint32_t kRow = 16u * T::ROW_CHUNKS;  // bytes per stored k-row
+      const char* p = area + off;
+      const i16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + kRow * 16 * ks));
+      const i16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + kRow * (16 * ks + 4)));
       return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   };
@@ -272,9 +296,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   };
   auto read = [&](const char* st, int ks, Frag& f) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < P::TM; ++i) f.a[i] = frag(SA{}, st, a_r[i], ks);
+    for (int i = 0; i < P::TM; ++i) f.a[i] = frag(SA{}, st, a_r[i], tr_a[i], ks);
 #pragma unroll
-    for (int j = 0; j < P::TN; ++j) f.b[j] = frag(SB{}, st + P::A_BYTES, b_r[j], ks);
+    for (int j = 0; j < P::TN; ++j) f.b[j] = frag(SB{}, SB::kKC ? st + P::A_BYTES : st, b_r[j], tr_b[j], ks);
   };
   auto mma = [&](const Frag& f) __attribute__((always_inline)) {
 #pragma unroll
