@@ -107,6 +107,18 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Barrier between K steps, without the memory fence of __syncthreads.  The
+// wait before it (vmcnt(WAIT) lgkmcnt(0)) already completes this wave's
+// copies of the next step and its reads of the slot the next copies reuse;
+// a workgroup fence would in addition wait for every copy in flight
+// (vmcnt(0)), draining the ring of stage buffers at each step.  The empty
+// asm statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void step_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Scheduling groups "1 MFMA, then its share of the IPS loads", NM times.
 template <int NM, int IPS, int X = 0>
 __device__ __forceinline__ void sched_mfma_vmem() {
@@ -355,7 +367,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     __builtin_amdgcn_sched_barrier(0);
     // vmcnt(WAIT) lgkmcnt(0) (gfx9 encoding, expcnt unconstrained)
     __builtin_amdgcn_s_waitcnt((WAIT & 15) | ((WAIT >> 4) << 14) | (7 << 4));
-    __syncthreads();
+    step_barrier();
     read(buf(std::integral_constant<int, (i + 1) % NBUF>{}), 0, f[0]);
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -367,7 +379,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     if constexpr (NBUF > 2) dma(1, lds1);
     if constexpr (NBUF > 3) dma(2, lds2);
     wait_vmcnt<WAIT>();
-    __syncthreads();
+    step_barrier();
     read(lds0, 0, f[0]);
   }
   int kt = 0;
@@ -441,6 +453,7 @@ TILEC_LDS_VARIANT(256, 256, 64, 2, 2, 4)
 TILEC_LDS_VARIANT(256, 128, 64, 3, 4, 2)
 TILEC_LDS_VARIANT(256, 128, 32, 4, 2, 2)
 TILEC_LDS_VARIANT(128, 128, 64, 4, 2, 4)
+TILEC_LDS_VARIANT(256, 256, 32, 4, 2, 4)
 #undef TILEC_LDS_VARIANT
 
 }  // namespace tilec
