@@ -206,7 +206,7 @@ def test_skinny_fma_path():
     N, row- and column-major x1, split K, against the fp64 oracle; small
     integers bit-exact."""
     fma = [v for v in _lib.variants() if v["family"] == _lib.FAMILY_SKINNY and v["max_m"]]
-    assert len(fma) == 8
+    assert len(fma) == 14  # 8 streaming FMA variants, 6 row-dot variants for x @ W.T
     for v in fma:
         bf = v["dtype"] == _lib.BF16
         for m in range(1, v["max_m"] + 1):
@@ -521,6 +521,52 @@ def test_gemv_weight_transposed(m):
     got16 = run(dev_bf16(x16), dev_bf16(w16).t())
     assert O.rel_l2(got16, O.matmul_bf16_f64(x16, np.ascontiguousarray(w16.T))) <= 1e-5
     say(f"gemv x @ W.T m={m} ok")
+
+
+def test_gemv_rows_kernel():
+    """The row-dot kernel for x @ W.T (x2 column-major: W [N, K] row-major,
+    one wave per one or two rows of W over all of K, no K split): every M up to the
+    variant's bound, N ragged against the rows per workgroup, K a multiple of
+    the 16-byte group but not of the 1 KiB wave chunk, a W row stride past K
+    whose padding holds NaN (rows are masked at K, so it must not leak),
+    against the fp64 oracle; small integers bit-exact; other layouts run the
+    streaming kernel."""
+    rows = [v for v in _lib.variants() if ext.rows_variant(v)]
+    assert len(rows) == 6
+    for v in rows:
+        bf = v["dtype"] == _lib.BF16
+        for m in range(1, v["max_m"] + 1):
+            for i, (k, n) in enumerate([(8, 1), (1000, 37), (4096, 513), (2056, 130)]):
+                a, w = O.normal((m, k), 60 * m + i), O.normal((n, k), 60 * m + i + 30)
+                if bf:
+                    a, w = O.bf16_round(a), O.bf16_round(w)
+                ref = (O.matmul_bf16_f64 if bf else O.matmul_f64)(a, np.ascontiguousarray(w.T))
+                pad = np.full((n, k + 24), np.nan, dtype=w.dtype if not bf else np.float32)
+                if bf:
+                    wp = np.full((n, k + 24), 0x7FC0, dtype=np.uint16)  # bf16 NaN
+                    wp[:, :k] = w
+                    dw, dx = dev_bf16(wp)[:, :k], dev_bf16(a)
+                else:
+                    pad[:, :k] = w
+                    dw, dx = dev(pad)[:, :k], dev(a)
+                assert dw.stride() == (k + 24, 1)
+                say(f"{v['name']} m={m} k={k} n={n}")
+                got = run(dx, dw.t(), (v["name"], 1))
+                assert O.rel_l2(got, ref) <= (1e-5 if bf else O.TOL_F32), (v["name"], m, k, n)
+                assert np.isfinite(got).all()
+    rng = np.random.default_rng(33)
+    for m in (1, 3, 4):
+        a = rng.integers(-3, 4, (m, 3000)).astype(np.float32)
+        w = rng.integers(-3, 4, (260, 3000)).astype(np.float32)
+        want = (a.astype(np.int64) @ w.T.astype(np.int64)).astype(np.float32)
+        for v in rows:
+            if m > v["max_m"]:
+                continue
+            conv = (lambda x: dev(x).to(torch.bfloat16)) if v["dtype"] == _lib.BF16 else dev
+            np.testing.assert_array_equal(run(conv(a), conv(w).t(), (v["name"], 1)), want)
+            for layout in (0, _lib.X1_COL_MAJOR, _lib.X1_COL_MAJOR | _lib.X2_COL_MAJOR):
+                got = run_layout(conv(a), conv(np.ascontiguousarray(w.T)), layout, (v["name"], 2))
+                np.testing.assert_array_equal(got, want)
 
 
 def test_non_default_stream_and_ordering():

@@ -565,6 +565,130 @@ hipError_t launch_skinny(const MatmulArgs& a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Row-dot kernel for x @ W.T: x2 column-major, i.e. the rows of W [N, K]
+// (row stride ldx2) are the columns of x2, and out[m][n] = sum_k x1[m][k] *
+// W[n][k].  Each wave owns RPW rows of W (RPW output columns) for the whole
+// of K, so there is no K split and no cross-workgroup combine: a row is a
+// contiguous run of K elements, read in 1 KiB wave loads (lane l takes
+// elements EPL*l .. of each 64*EPL chunk), dotted with the matching x1
+// pieces in FMAs (M <= MR rows of x1, row-major, from the cache), and the 64
+// lanes meet in a butterfly at the end.  Rows past N and elements past K are
+// masked by the buffer resources' extents (one resource per row, num_records
+// = K elements): they load zeros.  No LDS, no barriers.
+// ---------------------------------------------------------------------------
+template <typename T, int MR, int RPW, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restrict__ x1, const T* __restrict__ w,
+                                                               float* __restrict__ out, int M, int N, int K,
+                                                               int64_t ldx1, int64_t ldw, int64_t ldo) {
+  constexpr int EPL = 16 / (int)sizeof(T);  // elements per 16-byte load
+  constexpr int CH = 64 * EPL;             // K elements per wave load
+  typedef std::conditional_t<sizeof(T) == 4, f32x4, i32x4> V;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = (blockIdx.x * WAVES + wave) * RPW;
+  if (row0 >= N) return;
+  const uint32_t kbytes = (uint32_t)K * sizeof(T);
+  BufRsrc rw[RPW], rx[MR];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) rw[r] = make_rsrc(w + (int64_t)(row0 + r) * ldw, row0 + r < N ? kbytes : 0u);
+#pragma unroll
+  for (int m = 0; m < MR; ++m) rx[m] = make_rsrc(x1 + (int64_t)m * ldx1, m < M ? kbytes : 0u);
+  auto ld = [&](const BufRsrc& rs, uint32_t off) -> V {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+  };
+  auto elem = [](const V& v, int e) -> float {
+    if constexpr (sizeof(T) == 4) return v[e];
+    else return (e & 1) ? bf16_hi(v[e >> 1]) : bf16_lo(v[e >> 1]);
+  };
+  struct Batch {
+    V w[U][RPW], x[U][MR];
+  };
+  float acc[RPW][MR];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[r][m] = 0.f;
+  const uint32_t lane_off = 16u * (uint32_t)lane;
+  auto load = [&](int c0, Batch& b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // chunk c0 + u; past K every element is masked (offset >= extent)
+      const uint32_t off = (uint32_t)(c0 + u) * (uint32_t)CH * sizeof(T) + lane_off;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) b.w[u][r] = ld(rw[r], off);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) b.x[u][m] = ld(rx[m], off);
+    }
+  };
+  auto fma = [&](const Batch& b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const float xv = elem(b.x[u][m], e);
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) acc[r][m] = __builtin_fmaf(elem(b.w[u][r], e), xv, acc[r][m]);
+        }
+  };
+  const int nch = (K + CH - 1) / CH;
+  const int nb = (nch + U - 1) / U;
+  Batch A, B;
+  if (nb > 0) load(0, A);
+  for (int i = 0; i + 1 < nb; i += 2) {
+    load((i + 1) * U, B);
+    __builtin_amdgcn_sched_barrier(0);
+    fma(A);
+    __builtin_amdgcn_sched_barrier(0);
+    load((i + 2) * U, A);
+    __builtin_amdgcn_sched_barrier(0);
+    fma(B);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (nb & 1) fma(A);
+  // Butterfly over the 64 lanes; every lane ends with the full sums.
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float v = acc[r][m];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      acc[r][m] = v;
+    }
+  // Lane r * MR + m stores out[m][row0 + r].
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (lane == r * MR + m && m < M && row0 + r < N) out[(int64_t)m * ldo + row0 + r] = acc[r][m];
+}
+
+// x @ W.T with a 16-byte aligned row-major x1 and W (K and both strides
+// multiples of the 16-byte element count), M <= MR: the row-dot kernel; any
+// other layout or alignment runs the streaming kernel's variant FB.
+template <typename T, int MR, int RPW, int WAVES, int U, typename FB>
+hipError_t launch_rows(const MatmulArgs& a, FB fallback) {
+  constexpr int EPL = 16 / (int)sizeof(T);
+  auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool fits = (a.layout & 3) == TILEC_X2_COL_MAJOR && a.M <= MR && a.K % EPL == 0 && a.ldx1 % EPL == 0 &&
+                    a.ldx2 % EPL == 0 && aligned(a.x1) && aligned(a.x2) &&
+                    (int64_t)a.K * (int64_t)sizeof(T) < (int64_t(1) << 31) - 64;
+  if (!fits) return fallback(a);
+  const int64_t rows_per_wg = (int64_t)WAVES * RPW;
+  hipLaunchKernelGGL((gemv_rows_kernel<T, MR, RPW, WAVES, U>), dim3((unsigned)cdiv(a.N, rows_per_wg)), dim3(WAVES * 64),
+                     0, a.stream, static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out, (int)a.M, (int)a.N,
+                     (int)a.K, a.ldx1, a.ldx2, a.ldo);
+  return hipGetLastError();
+}
+
+template <typename T, int MR, int RPW, int WAVES, int U>
+hipError_t launch_rows_or_skinny(const MatmulArgs& a) {
+  return launch_rows<T, MR, RPW, WAVES, U>(a, [](const MatmulArgs& b) { return launch_skinny<T, 4, 2>(b); });
+}
+
 }  // namespace
 
 // Variant table for this family (its order is part of the variant numbering).
@@ -590,6 +714,14 @@ const VariantDesc* skinny_variants(int* count) {
       {"skinny_bf16_v1_w8_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 8, 1, 2, launch_skinny<u16, 8, 2, 1>},
       {"skinny_bf16_v4_w4_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 4, 4, 2, launch_skinny<u16, 4, 2, 4>},
       {"skinny_bf16_v4_w8_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 8, 4, 2, launch_skinny<u16, 8, 2, 4>},
+      // x @ W.T (column-major x2): row-dot kernel, one or two W rows per wave, no K split (other
+      // layouts run skinny_*_w4_b2).  BN = W rows per workgroup.
+      {"skinny_f32_t1_r1_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 4, kKcMax, 4, 1, 4, launch_rows_or_skinny<float, 1, 1, 4, 4>},
+      {"skinny_f32_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<float, 1, 2, 4, 4>},
+      {"skinny_f32_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<float, 4, 2, 4, 2>},
+      {"skinny_bf16_t1_r1_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 4, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 1, 4, 4>},
+      {"skinny_bf16_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 2, 4, 4>},
+      {"skinny_bf16_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<u16, 4, 2, 4, 2>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

@@ -110,7 +110,14 @@ size_t gemm_counter_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K,
 
 // Built-in rule (used when the caller passes TILEC_VARIANT_AUTO).
 int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2, int layout) {
-  (void)K;
+  // x @ W.T with M <= 4: the row-dot kernel (no K split; it runs the
+  // streaming kernel itself when the operands are not 16-byte aligned).
+  const int64_t epl = dtype == TILEC_F32 ? 4 : 8;  // elements per 16-byte load
+  if ((layout & 3) == TILEC_X2_COL_MAJOR && M >= 1 && M <= 4 && K % epl == 0 && ldx1 % epl == 0 &&
+      ldx2 % epl == 0 && skinny_fits(ldx1, ldx2, layout)) {
+    if (dtype == TILEC_F32) return find(M == 1 ? "skinny_f32_t1_r1_w4" : "skinny_f32_t4_r2_w4");
+    return find(M == 1 ? "skinny_bf16_t1_r2_w4" : "skinny_bf16_t4_r2_w4");
+  }
   if (dtype == TILEC_F32) {
     if ((M <= 16 || small_output(M, N)) && cdiv(M, 16) <= kSkinnyMaxRowBlocks && skinny_fits(ldx1, ldx2, layout))
       return find("skinny_f32_w8_b1");

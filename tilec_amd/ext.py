@@ -17,6 +17,8 @@ present.  The legacy config-space helpers of the reference (`plan`,
 `mm_configs`, ...) are kept with their original meaning.
 """
 
+import re
+
 import torch
 
 from . import _lib
@@ -72,8 +74,13 @@ def mm_configs(M1, N, M2):
 _SKINNY_SPLITS = (1, 2, 4, 8, 16, 32, 64)
 
 
-def hip_configs(M, K, N, dtype="f32"):
+def hip_configs(M, K, N, dtype="f32", layout=None):
     """Every (variant, split_k) the library can run for out[M,N] = x1[M,K]·x2[K,N].
+
+    The row-dot variants are offered only where their kernel runs: K a
+    multiple of the 16-byte element count and, with `layout` given, x @ W.T
+    (x2 column-major, x1 row-major).  Elsewhere they run the streaming
+    kernel unsplit, which is never the config to pick.
 
     The skinny family (a K split, 16-row blocks) is offered for M <= 16 and,
     for fp32, outputs too small to fill the chip with 64x64 tiles; the tile GEMMs
@@ -89,7 +96,11 @@ def hip_configs(M, K, N, dtype="f32"):
             continue
         if v["family"] == _lib.FAMILY_SKINNY and not skinny_regime(M, N, code):
             continue
-        if v["family"] == _lib.FAMILY_SKINNY:
+        if v["family"] == _lib.FAMILY_SKINNY and rows_variant(v):
+            epl = 4 if code == _lib.F32 else 8  # elements per 16-byte load
+            if K % epl == 0 and (layout is None or layout == _lib.X2_COL_MAJOR):
+                out.append((v["name"], 1))  # the row-dot kernel never splits K
+        elif v["family"] == _lib.FAMILY_SKINNY:
             # A workgroup takes at most BK (the variant's K-slice cap) rows
             # of K, so small splits are raised; keep one entry per distinct
             # effective split, each giving every wave at least one 16-row block.
@@ -116,6 +127,13 @@ def hip_configs(M, K, N, dtype="f32"):
 
 _GEMM_SPLITS = (2, 4, 8, 16)
 SPLIT_MAX_ACC_PER_THREAD = 64  # tilec_amd/csrc/common.h, kSplitMaxAccPerThread
+
+
+def rows_variant(v):
+    """Variants named *_t<MR>_r<RPW>_* run the row-dot kernel for x @ W.T
+    (csrc/skinny.hip, gemv_rows_kernel): one wave per 1-2 rows of W over all
+    of K, no K split; other layouts run the streaming kernel."""
+    return re.search(r"_t\d+_r\d+_", v["name"]) is not None
 
 
 def prep_variant(v):

@@ -217,10 +217,12 @@ def _draw(rng):
     return None
 
 
-def shapes(n=500, seed=0, n_layout=120):
+def shapes(n=500, seed=0, n_layout=120, n_rows=40):
     """Seeded random shapes (M, K, N, dtype, layout): `n` row-major draws plus
-    CONFIG_SHAPES, and `n_layout` draws of a second stream (seed + 1) with a
-    random non-row-major layout, plus LAYOUT_CONFIG_SHAPES."""
+    CONFIG_SHAPES, `n_layout` draws of a second stream (seed + 1) with a
+    random non-row-major layout, plus LAYOUT_CONFIG_SHAPES, and `n_rows`
+    x @ W.T shapes with M <= 4 from a third stream (seed + 2), the row-dot
+    kernel's domain."""
     rng = random.Random(seed)
     out = set(CONFIG_SHAPES)
     while len(out) < n + len(CONFIG_SHAPES):
@@ -234,7 +236,16 @@ def shapes(n=500, seed=0, n_layout=120):
         d = _draw(rng2)
         if d is not None:
             lay.add(d + (rng2.choice((1, 2, 2, 3)),))  # x @ W.T (x2 column-major) twice as often
-    return sorted(out | lay, key=lambda s: (s[0] * s[1] * s[2], s))
+    rng3 = random.Random(seed + 2)
+    rows = set()
+    while len(rows) < n_rows:
+        M, K, N = rng3.randint(1, 4), round(2 ** rng3.uniform(8, 14)), round(2 ** rng3.uniform(8, 14))
+        if rng3.random() < 0.5:
+            K = 1 << round(math.log2(K))
+        dtype = rng3.choice(("f32", "bf16"))
+        if K * N <= 1 << 26:
+            rows.add((M, K, N, dtype, _lib.X2_COL_MAJOR))
+    return sorted(out | lay | rows, key=lambda s: (s[0] * s[1] * s[2], s))
 
 
 def operands(M, K, N, dtype, layout, gen):
@@ -283,7 +294,7 @@ def bench(n=300, seed=0, path=None):
         todo = shapes(n, seed)
         for i, (M, K, N, dtype, layout) in enumerate(todo):
             have = timed_cfgs.get((M, K, N, dtype, layout), {})
-            missing = [c for c in ext.hip_configs(M, K, N, dtype) if c not in have]
+            missing = [c for c in ext.hip_configs(M, K, N, dtype, layout) if c not in have]
             if not missing:
                 continue  # resumable: only configs not yet timed (e.g. new variants)
             x1, x2 = operands(M, K, N, dtype, layout, g)
@@ -317,9 +328,14 @@ def train(test_frac=0.2, seed=0, out=MODEL, path=None):
     library's built-in rule, refit on everything and export JSON
     (tilec/tune.py:99-132)."""
     from sklearn.ensemble import GradientBoostingRegressor
+    from . import ext
     rows = load(path)
     names = _variant_by_name()
-    rows = [r for r in rows if r["kernel"] in names]
+    # only the configs hip_configs offers for the row's layout (the row-dot
+    # variants only for x @ W.T)
+    rows = [r for r in rows if r["kernel"] in names and
+            (not ext.rows_variant(names[r["kernel"]]) or
+             (r["kernel"], int(r["split_k"])) in ext.hip_configs(*_key(r)[:4], int(r["layout"])))]
     keys = sorted({_key(r) for r in rows})
     random.Random(seed).shuffle(keys)
     test = set(keys[:int(len(keys) * test_frac)])
@@ -447,7 +463,7 @@ def pick(M, K, N, dtype="f32", layout=0):
     if model is None or 0 in (M, K, N):
         return None
     from . import ext
-    cands = ext.hip_configs(M, K, N, dtype)
+    cands = ext.hip_configs(M, K, N, dtype, layout)
     if not cands:
         return None
     measured = model.best.get((M, K, N, dtype, layout))
