@@ -105,20 +105,22 @@ __device__ bool split_tail(float& val, int V, int split, int S, int cell, int ce
 // raw (bf16 as pairs, low half first): elements at or past n load zeros.
 // VEC: n and c are multiples of E, one 16-byte load; otherwise element by
 // element.
+// The matrix is read once: loads carry the non-temporal cache policy.
+constexpr int kCpolNt = 2;
 template <typename T, bool VEC>
 __device__ __forceinline__ i32x4 load_group(const BufRsrc& rs, uint32_t row_off, int c, int n) {
   constexpr int E = 16 / (int)sizeof(T);
   constexpr uint32_t EB = sizeof(T);
   if constexpr (VEC) {
     const uint32_t off = c < n ? row_off + (uint32_t)c * EB : kOob;
-    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, kCpolNt));
   } else {
     int h[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const uint32_t off = c + e < n ? row_off + (uint32_t)(c + e) * EB : kOob;
-      if constexpr (E == 4) h[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
-      else h[e] = (int)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0);
+      if constexpr (E == 4) h[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, kCpolNt);
+      else h[e] = (int)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, kCpolNt);
     }
     i32x4 w;
 #pragma unroll

@@ -62,6 +62,10 @@ constexpr int kMaxM = 16;      // MFMA rows
 constexpr int kBlock = 16;     // K chunks are whole multiples of 16 rows
 constexpr int kKcMax = 1024;   // rows per K chunk at most
 constexpr int kCounterStride = 64;  // uint32s between completion counters (own 256-byte line each)
+// Cache policy of the x2 loads: non-temporal (x2 is streamed once; keeping
+// it out of the way of x1 and the partials in L2 took 6-10 % off the fp32
+// GEMV at K = N = 4096).
+constexpr int kCpolX2 = 2;
 
 typedef unsigned short u16;  // bf16 bit pattern
 typedef int i32x2 __attribute__((ext_vector_type(2)));
@@ -246,8 +250,8 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
         const uint32_t roff = EB * (uint32_t)row * (uint32_t)ldx2;
         if constexpr (VEC) {
           const uint32_t o = (ok & col_ok) ? roff + col_off : kOob;
-          if constexpr (CPL == 4) blk.b[u] = load_f32x4(rx2, o);
-          else blk.b[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, 0));
+          if constexpr (CPL == 4) blk.b[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, kCpolX2));
+          else blk.b[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, kCpolX2));
         } else {
           int h[CPL];
 #pragma unroll
@@ -304,7 +308,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
         const uint32_t noff = EB * ((uint32_t)n * (uint32_t)ldx2 + (uint32_t)kr);
         if constexpr (VEC) {  // K % EPL == 0: a lane's EPL k are all valid or all past the chunk
           const uint32_t o = (nok & (brow + kr < nrows)) ? noff : kOob;
-          blk.b[g] = __builtin_bit_cast(decltype(blk.a), __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, 0));
+          blk.b[g] = __builtin_bit_cast(decltype(blk.a), __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, kCpolX2));
         } else {
           int h[EPL];
 #pragma unroll
@@ -575,9 +579,10 @@ hipError_t launch_skinny(const MatmulArgs& a) {
 // pieces in FMAs (M <= MR rows of x1, row-major, from the cache), and the 64
 // lanes meet in a butterfly at the end.  Rows past N and elements past K are
 // masked by the buffer resources' extents (one resource per row, num_records
-// = K elements): they load zeros.  No LDS, no barriers.
+// = K elements): they load zeros.  W is read with the non-temporal cache
+// policy CP (streamed once); x1 stays cached.  No LDS, no barriers.
 // ---------------------------------------------------------------------------
-template <typename T, int MR, int RPW, int WAVES, int U>
+template <typename T, int MR, int RPW, int WAVES, int U, int CP>
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restrict__ x1, const T* __restrict__ w,
                                                                float* __restrict__ out, int M, int N, int K,
                                                                int64_t ldx1, int64_t ldw, int64_t ldo) {
@@ -596,6 +601,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
   for (int m = 0; m < MR; ++m) rx[m] = make_rsrc(x1 + (int64_t)m * ldx1, m < M ? kbytes : 0u);
   auto ld = [&](const BufRsrc& rs, uint32_t off) -> V {
     return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+  };
+  auto ld_w = [&](const BufRsrc& rs, uint32_t off) -> V {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, CP));
   };
   auto elem = [](const V& v, int e) -> float {
     if constexpr (sizeof(T) == 4) return v[e];
@@ -616,7 +624,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
       // chunk c0 + u; past K every element is masked (offset >= extent)
       const uint32_t off = (uint32_t)(c0 + u) * (uint32_t)CH * sizeof(T) + lane_off;
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) b.w[u][r] = ld(rw[r], off);
+      for (int r = 0; r < RPW; ++r) b.w[u][r] = ld_w(rw[r], off);
 #pragma unroll
       for (int m = 0; m < MR; ++m) b.x[u][m] = ld(rx[m], off);
     }
@@ -669,7 +677,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
 // x @ W.T with a 16-byte aligned row-major x1 and W (K and both strides
 // multiples of the 16-byte element count), M <= MR: the row-dot kernel; any
 // other layout or alignment runs the streaming kernel's variant FB.
-template <typename T, int MR, int RPW, int WAVES, int U, typename FB>
+template <typename T, int MR, int RPW, int WAVES, int U, int CP, typename FB>
 hipError_t launch_rows(const MatmulArgs& a, FB fallback) {
   constexpr int EPL = 16 / (int)sizeof(T);
   auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -678,7 +686,7 @@ hipError_t launch_rows(const MatmulArgs& a, FB fallback) {
                     (int64_t)a.K * (int64_t)sizeof(T) < (int64_t(1) << 31) - 64;
   if (!fits) return fallback(a);
   const int64_t rows_per_wg = (int64_t)WAVES * RPW;
-  hipLaunchKernelGGL((gemv_rows_kernel<T, MR, RPW, WAVES, U>), dim3((unsigned)cdiv(a.N, rows_per_wg)), dim3(WAVES * 64),
+  hipLaunchKernelGGL((gemv_rows_kernel<T, MR, RPW, WAVES, U, CP>), dim3((unsigned)cdiv(a.N, rows_per_wg)), dim3(WAVES * 64),
                      0, a.stream, static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out, (int)a.M, (int)a.N,
                      (int)a.K, a.ldx1, a.ldx2, a.ldo);
   return hipGetLastError();
@@ -686,7 +694,7 @@ hipError_t launch_rows(const MatmulArgs& a, FB fallback) {
 
 template <typename T, int MR, int RPW, int WAVES, int U>
 hipError_t launch_rows_or_skinny(const MatmulArgs& a) {
-  return launch_rows<T, MR, RPW, WAVES, U>(a, [](const MatmulArgs& b) { return launch_skinny<T, 4, 2>(b); });
+  return launch_rows<T, MR, RPW, WAVES, U, kCpolX2>(a, [](const MatmulArgs& b) { return launch_skinny<T, 4, 2>(b); });
 }
 
 }  // namespace
