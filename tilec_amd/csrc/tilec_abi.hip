@@ -112,6 +112,9 @@ size_t gemm_counter_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K,
 int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2, int layout) {
   // x @ W.T with M <= 4: the row-dot kernel (no K split; it runs the
   // streaming kernel itself when the operands are not 16-byte aligned).
+  // Its workspace and counter needs (those of that fallback, unsplit) never
+  // exceed those of the streaming variant chosen below for the same shape in
+  // another layout, so sizes queried with TILEC_VARIANT_AUTO still suffice.
   const int64_t epl = dtype == TILEC_F32 ? 4 : 8;  // elements per 16-byte load
   if ((layout & 3) == TILEC_X2_COL_MAJOR && M >= 1 && M <= 4 && K % epl == 0 && ldx1 % epl == 0 &&
       ldx2 % epl == 0 && skinny_fits(ldx1, ldx2, layout)) {
