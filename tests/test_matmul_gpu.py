@@ -649,3 +649,41 @@ def test_graph_capture_replays():
         assert torch.equal(out2, eager2), i
         del junk
     say("graph replay ok")
+
+
+def test_graph_capture_row_dot_and_bf16_rings():
+    """The kernels without a K split in a captured graph: the row-dot kernel
+    for x @ W.T and the bf16 LDS-DMA GEMM with a ring of four stage buffers
+    (fence-free step barrier), replayed several times with eager work
+    between replays; every replay must match the eager result bit for bit."""
+    x, w = O.normal((1, 2048), 70), O.normal((1536, 2048), 71)
+    a16, b16 = O.bf16_round(O.normal((512, 1024), 72)), O.bf16_round(O.normal((1024, 512), 73))
+    dx, dw = dev(x), dev(w)
+    da, db = dev_bf16(a16), dev_bf16(b16)
+    cfg_rows, cfg_ring = ("skinny_f32_t1_r1_w4", 1), ("gemm_bf16_256x256x32_r4w8", 1)
+    eager = ext.matrix_mul(dx, dw.t(), cfg_rows)
+    eager2 = ext.matrix_mul(da, db, cfg_ring)
+    torch.cuda.synchronize()
+    assert O.rel_l2(eager.cpu().numpy(), O.matmul_f64(x, np.ascontiguousarray(w.T))) <= O.TOL_F32
+    assert O.rel_l2(eager2.cpu().numpy(), O.matmul_bf16_f64(a16, b16)) <= 1e-5
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ext.matrix_mul(dx, dw.t(), cfg_rows)
+        ext.matrix_mul(da, db, cfg_ring)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            out = ext.matrix_mul(dx, dw.t(), cfg_rows)
+            out2 = ext.matrix_mul(da, db, cfg_ring)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(4):
+        out.zero_()
+        out2.zero_()
+        g.replay()
+        junk = ext.matrix_mul(da[:64], db)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        assert torch.equal(out2, eager2), i
+        del junk
+    say("graph replay (row-dot, bf16 ring of 4) ok")
