@@ -44,6 +44,9 @@
 //
 // Grid: x = slabs of 16*CPL columns, y = K splits, z = 16-row blocks of x1
 // and out.
+//
+// x @ W.T with M <= 4 has a second kernel below, gemv_rows_kernel: one wave
+// per row of W over all of K, no K split.
 // Waves are summed through LDS; with a split K each workgroup writes its
 // [16 x SLAB] partial to the workspace, and the last workgroup of a (row
 // block, slab) to finish (completion counter) adds the partials in split
@@ -62,9 +65,8 @@ constexpr int kMaxM = 16;      // MFMA rows
 constexpr int kBlock = 16;     // K chunks are whole multiples of 16 rows
 constexpr int kKcMax = 1024;   // rows per K chunk at most
 constexpr int kCounterStride = 64;  // uint32s between completion counters (own 256-byte line each)
-// Cache policy of the x2 loads: non-temporal (x2 is streamed once; keeping
-// it out of the way of x1 and the partials in L2 took 6-10 % off the fp32
-// GEMV at K = N = 4096).
+// Cache policy of the x2 loads: non-temporal, as x2 is streamed once (the
+// hint took 6-10 % off the fp32 GEMV at K = N = 4096).
 constexpr int kCpolX2 = 2;
 
 typedef unsigned short u16;  // bf16 bit pattern
