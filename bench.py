@@ -129,10 +129,10 @@ def bench_square(args):
     return dict(ms=ms, tflops=tflops, config=cfg)
 
 
-def _gemv(x1, x2s, steps, mm=None):
+def _gemv(x1, x2s, steps, mm=None, settle_ms=0.0):
     """us per launch of mm(x1, x2s[i]) (default ext.matrix_mul) over rotating
     x2 buffers, launches replayed from a HIP graph (an ~8 us kernel is not
-    host-bound)."""
+    host-bound), after `settle_ms` of untimed replays."""
     import torch
     from tilec_amd import ext
     mm = mm or ext.matrix_mul
@@ -152,7 +152,7 @@ def _gemv(x1, x2s, steps, mm=None):
     torch.cuda.synchronize()
     replays = max(1, steps // reps)
     with torch.cuda.stream(s):
-        ms = timed(g.replay, replays, 2, stream=s) / reps
+        ms = timed(g.replay, replays, 2, stream=s, settle_ms=settle_ms) / reps
     del outs
     return ms * 1e3
 
@@ -178,7 +178,7 @@ def _gemv_cases(ms_by_dtype, transposed, steps):
             x1 = torch.from_numpy(O.normal((M, K), 2)).to(tdt).cuda()
             assert ext.layout_of(x1, x2s[0]) == (2 if transposed else 0)
             cfg = kernel_name_for(M, K, N, dtype, 2 if transposed else 0)
-            us = _gemv(x1, x2s, steps)
+            us = _gemv(x1, x2s, steps, settle_ms=SETTLE_MS / 2)
             nbytes = esz * (M * K + K * N) + 4 * M * N
             gbs = nbytes / (us * 1e-6) / 1e9
             key = (f"M{M}" if dtype == "f32" else f"bf16_M{M}")

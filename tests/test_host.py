@@ -125,9 +125,9 @@ def test_gemm_split_geometry_matches_the_library():
 
 
 def test_row_dot_configs_only_where_the_kernel_runs():
-    """The row-dot variants (x @ W.T) are offered unsplit, for x2 column-major
-    and K a multiple of the 16-byte group; elsewhere they would run the
-    streaming kernel unsplit."""
+    """The x @ W.T variants (row-dot, M <= 4; row-tile, M <= 16) are offered
+    unsplit, for x2 column-major and K a multiple of the 16-byte group;
+    elsewhere they would run the streaming kernel unsplit."""
     rows = lambda cfgs: [c for c in cfgs if ext.rows_variant(_lib.variants()[_lib.variant_id(c[0])])]
     f32 = rows(ext.hip_configs(1, 4096, 4096, "f32", _lib.X2_COL_MAJOR))
     assert f32 and all(s == 1 for _, s in f32)
@@ -136,7 +136,10 @@ def test_row_dot_configs_only_where_the_kernel_runs():
     assert not rows(ext.hip_configs(1, 4096, 4096, "f32", _lib.X1_COL_MAJOR | _lib.X2_COL_MAJOR))
     assert not rows(ext.hip_configs(1, 4094, 4096, "f32", _lib.X2_COL_MAJOR))
     assert not rows(ext.hip_configs(1, 4092, 4096, "bf16", _lib.X2_COL_MAJOR))
-    assert not rows(ext.hip_configs(5, 4096, 4096, "f32", _lib.X2_COL_MAJOR))  # M above every bound
+    m5 = rows(ext.hip_configs(5, 4096, 4096, "f32", _lib.X2_COL_MAJOR))
+    assert m5 and all(c.endswith(("_c1k", "_c512")) for c, _ in m5)  # only the row-tile kernel above M = 4
+    assert rows(ext.hip_configs(16, 4096, 4096, "bf16", _lib.X2_COL_MAJOR))
+    assert not rows(ext.hip_configs(17, 4096, 4096, "f32", _lib.X2_COL_MAJOR))  # M above every bound
 
 
 def test_tune_features_and_shapes():
@@ -144,14 +147,16 @@ def test_tune_features_and_shapes():
     assert len(f) == 19 and all(math.isfinite(x) for x in f) and f[-3:-1] == [0.0, 0.0]
     assert tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8, layout=3)[-3:-1] == [1.0, 1.0]
     assert tune.features(1, 4096, 4096, 256, "f32", "skinny_f32_v1_w4_b2", 4)[-1] == 1.0
-    s = tune.shapes(120, seed=0, n_layout=40, n_rows=10)
-    assert s == tune.shapes(120, seed=0, n_layout=40, n_rows=10)
+    s = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6)
+    assert s == tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6)
     rm = [x for x in s if x[4] == 0]
     lay = [x for x in s if x[4] != 0]
-    assert len(rm) == 120 + len(tune.CONFIG_SHAPES) and len(lay) == 40 + len(tune.LAYOUT_CONFIG_SHAPES) + 10
-    # the x @ W.T stream (M <= 4, x2 column-major) adds to, and does not change, the others
-    no_rows = tune.shapes(120, seed=0, n_layout=40, n_rows=0)
+    assert len(rm) == 120 + len(tune.CONFIG_SHAPES) and len(lay) == 40 + len(tune.LAYOUT_CONFIG_SHAPES) + 10 + 6
+    # the x @ W.T streams (M <= 4 and 5 <= M <= 16, x2 column-major) add to, and do not change, the others
+    no_rows = tune.shapes(120, seed=0, n_layout=40, n_rows=0, n_tile=6)
     assert set(no_rows) <= set(s) and all(x[0] <= 4 and x[4] == 2 for x in set(s) - set(no_rows))
+    no_tile = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=0)
+    assert set(no_tile) <= set(s) and all(5 <= x[0] <= 16 and x[4] == 2 for x in set(s) - set(no_tile))
     assert {x + (0,) for x in tune.CONFIG_SHAPES} <= set(rm) and set(tune.LAYOUT_CONFIG_SHAPES) <= set(lay)
     assert {x[4] for x in lay} == {1, 2, 3}
     assert any(m <= 16 for m, *_ in s) and any(d == "bf16" for _, _, _, d, _ in s)

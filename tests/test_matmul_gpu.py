@@ -205,7 +205,9 @@ def test_skinny_fma_path():
     MFMA path): every M up to the variant's bound, ragged and aligned K and
     N, row- and column-major x1, split K, against the fp64 oracle; small
     integers bit-exact."""
-    fma = [v for v in _lib.variants() if v["family"] == _lib.FAMILY_SKINNY and v["max_m"]]
+    # (the row-tile variants for x @ W.T, M <= 16, are covered by test_gemv_rows_kernel)
+    fma = [v for v in _lib.variants() if v["family"] == _lib.FAMILY_SKINNY and v["max_m"]
+           and not v["name"].endswith(("_c512", "_c1k"))]
     assert len(fma) == 14  # 8 streaming FMA variants, 6 row-dot variants for x @ W.T
     for v in fma:
         bf = v["dtype"] == _lib.BF16
@@ -524,38 +526,44 @@ def test_gemv_weight_transposed(m):
 
 
 def test_gemv_rows_kernel():
-    """The row-dot kernel for x @ W.T (x2 column-major: W [N, K] row-major,
-    one wave per one or two rows of W over all of K, no K split): every M up to the
-    variant's bound, N ragged against the rows per workgroup, K a multiple of
-    the 16-byte group but not of the 1 KiB wave chunk, a W row stride past K
-    whose padding holds NaN (rows are masked at K, so it must not leak),
-    against the fp64 oracle; small integers bit-exact; other layouts run the
-    streaming kernel."""
+    """The kernels for x @ W.T (x2 column-major: W [N, K] row-major, no K
+    split): the row-dot kernel (one wave per one or two rows of W over all of
+    K, M <= 4) and the row-tile kernel (16 or 8 rows of W per workgroup, MFMAs
+    fed through LDS, M <= 16).  Many M up to the variant's bound, N ragged
+    against the rows per workgroup, K a multiple of the 16-byte group but not
+    of the wave chunk, row strides of W and x1 past K whose padding holds NaN
+    (both are masked at K, so it must not leak), against the fp64 oracle;
+    small integers bit-exact; other layouts run the streaming kernel."""
     rows = [v for v in _lib.variants() if ext.rows_variant(v)]
-    assert len(rows) == 6
+    assert len(rows) == 12
     for v in rows:
         bf = v["dtype"] == _lib.BF16
-        for m in range(1, v["max_m"] + 1):
+        ms = range(1, v["max_m"] + 1) if v["max_m"] <= 4 else (1, 2, 5, 8, 13, 16)
+        for m in ms:
             for i, (k, n) in enumerate([(8, 1), (1000, 37), (4096, 513), (2056, 130)]):
                 a, w = O.normal((m, k), 60 * m + i), O.normal((n, k), 60 * m + i + 30)
                 if bf:
                     a, w = O.bf16_round(a), O.bf16_round(w)
                 ref = (O.matmul_bf16_f64 if bf else O.matmul_f64)(a, np.ascontiguousarray(w.T))
-                pad = np.full((n, k + 24), np.nan, dtype=w.dtype if not bf else np.float32)
                 if bf:
                     wp = np.full((n, k + 24), 0x7FC0, dtype=np.uint16)  # bf16 NaN
                     wp[:, :k] = w
-                    dw, dx = dev_bf16(wp)[:, :k], dev_bf16(a)
+                    ap = np.full((m, k + 8), 0x7FC0, dtype=np.uint16)
+                    ap[:, :k] = a
+                    dw, dx = dev_bf16(wp)[:, :k], dev_bf16(ap)[:, :k]
                 else:
-                    pad[:, :k] = w
-                    dw, dx = dev(pad)[:, :k], dev(a)
-                assert dw.stride() == (k + 24, 1)
+                    wp = np.full((n, k + 24), np.nan, dtype=np.float32)
+                    wp[:, :k] = w
+                    ap = np.full((m, k + 8), np.nan, dtype=np.float32)
+                    ap[:, :k] = a
+                    dw, dx = dev(wp)[:, :k], dev(ap)[:, :k]
+                assert dw.stride() == (k + 24, 1) and (m == 1 or dx.stride() == (k + 8, 1))
                 say(f"{v['name']} m={m} k={k} n={n}")
                 got = run(dx, dw.t(), (v["name"], 1))
                 assert O.rel_l2(got, ref) <= (1e-5 if bf else O.TOL_F32), (v["name"], m, k, n)
                 assert np.isfinite(got).all()
     rng = np.random.default_rng(33)
-    for m in (1, 3, 4):
+    for m in (1, 3, 4, 9, 16):
         a = rng.integers(-3, 4, (m, 3000)).astype(np.float32)
         w = rng.integers(-3, 4, (260, 3000)).astype(np.float32)
         want = (a.astype(np.int64) @ w.T.astype(np.int64)).astype(np.float32)
@@ -652,38 +660,47 @@ def test_graph_capture_replays():
 
 
 def test_graph_capture_row_dot_and_bf16_rings():
-    """The kernels without a K split in a captured graph: the row-dot kernel
-    for x @ W.T and the bf16 LDS-DMA GEMM with a ring of four stage buffers
-    (fence-free step barrier), replayed several times with eager work
-    between replays; every replay must match the eager result bit for bit."""
+    """The kernels without a K split in a captured graph: the row-dot and
+    row-tile kernels for x @ W.T and the bf16 LDS-DMA GEMM with a ring of four
+    stage buffers (fence-free step barrier), replayed several times with eager
+    work between replays; every replay must match the eager result bit for
+    bit."""
     x, w = O.normal((1, 2048), 70), O.normal((1536, 2048), 71)
+    x12 = O.normal((12, 2048), 74)
     a16, b16 = O.bf16_round(O.normal((512, 1024), 72)), O.bf16_round(O.normal((1024, 512), 73))
-    dx, dw = dev(x), dev(w)
+    dx, dw, dx12 = dev(x), dev(w), dev(x12)
     da, db = dev_bf16(a16), dev_bf16(b16)
     cfg_rows, cfg_ring = ("skinny_f32_t1_r1_w4", 1), ("gemm_bf16_256x256x32_r4w8", 1)
+    cfg_tile = ("skinny_f32_t16_r16_w16_c512", 1)
     eager = ext.matrix_mul(dx, dw.t(), cfg_rows)
     eager2 = ext.matrix_mul(da, db, cfg_ring)
+    eager3 = ext.matrix_mul(dx12, dw.t(), cfg_tile)
     torch.cuda.synchronize()
     assert O.rel_l2(eager.cpu().numpy(), O.matmul_f64(x, np.ascontiguousarray(w.T))) <= O.TOL_F32
     assert O.rel_l2(eager2.cpu().numpy(), O.matmul_bf16_f64(a16, b16)) <= 1e-5
+    assert O.rel_l2(eager3.cpu().numpy(), O.matmul_f64(x12, np.ascontiguousarray(w.T))) <= O.TOL_F32
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         ext.matrix_mul(dx, dw.t(), cfg_rows)
         ext.matrix_mul(da, db, cfg_ring)
+        ext.matrix_mul(dx12, dw.t(), cfg_tile)
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=s):
             out = ext.matrix_mul(dx, dw.t(), cfg_rows)
             out2 = ext.matrix_mul(da, db, cfg_ring)
+            out3 = ext.matrix_mul(dx12, dw.t(), cfg_tile)
     torch.cuda.current_stream().wait_stream(s)
     for i in range(4):
         out.zero_()
         out2.zero_()
+        out3.zero_()
         g.replay()
         junk = ext.matrix_mul(da[:64], db)  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
         assert torch.equal(out2, eager2), i
+        assert torch.equal(out3, eager3), i
         del junk
-    say("graph replay (row-dot, bf16 ring of 4) ok")
+    say("graph replay (row-dot, row-tile, bf16 ring of 4) ok")

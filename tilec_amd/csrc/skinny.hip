@@ -676,6 +676,142 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
       if (lane == r * MR + m && m < M && row0 + r < N) out[(int64_t)m * ldo + row0 + r] = acc[r][m];
 }
 
+// ---------------------------------------------------------------------------
+// Row-tile kernel for x @ W.T with up to 16 rows of x1: the MFMA counterpart
+// of the row-dot kernel.  A workgroup owns R rows of W (R output columns,
+// R <= 16) for the whole of K; its waves take interleaved K chunks of CHB
+// bytes per row and meet once, in LDS, at the end: no K split, no partials.
+//
+// The MFMA wants W as its A operand with one W row per lane group (A[i][k]
+// on lane i + 16 * (k-slot group)), which a coalesced load of a W row does
+// not give.  So each wave reads its chunk of the R rows with contiguous
+// CHB-byte wave loads (lane l: bytes 16 * (l % LPR) of row l / LPR of the
+// load) into registers, writes them to its own LDS area (rows CHB + 16 bytes
+// apart: the 16-byte skew makes the operand reads below conflict-free), and
+// reads them back as MFMA operands: for each 64-byte k group t of the chunk,
+// lane l reads 16 bytes of row l % 16 at byte 64 t + 16 (l / 16).  The
+// matching x1 pieces, x1[l % 16][same k], come straight from the cache as the
+// B operand, so D[i][j] accumulates out[j][n0 + i]:
+//   fp32: the 16 bytes are k = 4 g + u (g = l / 16, u < 4), one
+//         v_mfma_f32_16x16x4f32 per u;
+//   bf16: the 16 bytes are 8 consecutive k, one v_mfma_f32_16x16x32_bf16.
+// Which k meets which MFMA slot does not matter to the sum as long as A and B
+// agree, and they do (same byte offsets in W's row and x1's row).
+//
+// Only a wave's own LDS area is written and read in the loop (LDS runs a
+// wave's operations in order), so the loop has no barrier.  Masking is on
+// addresses: W rows past N, x1 rows past M and k past K load zeros (both
+// operands, so NaN padding past K cannot leak in).  Rows of the LDS area past
+// R are never written; they only feed D rows that are not stored.  A ring of
+// NB register sets keeps the loads of NB - 1 chunks in flight while a chunk
+// is multiplied (NB = 1: none; the 16-wave variants rely on their 4 waves per
+// SIMD instead).  Summing the waves in a fixed order keeps results
+// independent of scheduling.
+// ---------------------------------------------------------------------------
+template <typename T, int WAVES, int CHB, int R, int NB>
+__global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict__ x1, const T* __restrict__ w,
+                                                             float* __restrict__ out, int M, int N, int K,
+                                                             int64_t ldx1, int64_t ldw, int64_t ldo) {
+  constexpr int LPR = CHB / 16;    // lanes per W row in one wave load
+  constexpr int RPI = 64 / LPR;    // W rows per wave load
+  constexpr int NLD = R / RPI;     // W wave loads per chunk
+  constexpr int KG = CHB / 64;     // 64-byte k groups per chunk
+  constexpr int PITCH = CHB + 16;  // LDS bytes per staged row
+  static_assert(CHB == 512 || CHB == 1024, "chunk of 512 or 1024 bytes per row");
+  static_assert(R <= 16 && R % RPI == 0, "R rows of W, whole wave loads");
+  typedef std::conditional_t<sizeof(T) == 4, f32x4, i32x4> V;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[WAVES * 16 * PITCH];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * R;
+  const int m0 = blockIdx.y * 16;
+  const int q = lane & 15, g = lane >> 4;
+  const uint32_t kbytes = (uint32_t)K * sizeof(T);
+  const uint32_t ldw_b = (uint32_t)ldw * sizeof(T), ldx1_b = (uint32_t)ldx1 * sizeof(T);
+  const BufRsrc rw = make_rsrc(w + (int64_t)n0 * ldw);
+  const BufRsrc rx = make_rsrc(x1 + (int64_t)m0 * ldx1);
+  const int wrow = lane / LPR;                     // row of a wave load this lane reads
+  const uint32_t wcol = 16u * (uint32_t)(lane % LPR);  // its byte within the row piece
+  const bool xrow = m0 + q < M;
+  const uint32_t xoff = (uint32_t)q * ldx1_b + 16u * (uint32_t)g;
+  unsigned char* const area = lds + wave * 16 * PITCH;
+
+  struct Batch {
+    V w[NLD], x[KG];
+  };
+  // x1 pieces of chunk c: lane l reads x1[m0 + l % 16][k group t, 16 bytes at 16 (l / 16)]
+  auto load_x = [&](int c, V* x) __attribute__((always_inline)) {
+    const uint32_t cb = (uint32_t)c * CHB;
+#pragma unroll
+    for (int t = 0; t < KG; ++t) {
+      const uint32_t kb = cb + 64u * t + 16u * g;
+      const bool ok = xrow && kb < kbytes;
+      x[t] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(ok ? xoff + cb + 64u * t : kOob), 0, 0));
+    }
+  };
+  auto load = [&](int c, Batch& b) __attribute__((always_inline)) {
+    const uint32_t cb = (uint32_t)c * CHB;
+    const bool kw = cb + wcol < kbytes;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int r = i * RPI + wrow;
+      const bool ok = kw && n0 + r < N;
+      b.w[i] = __builtin_bit_cast(
+          V, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ok ? (uint32_t)r * ldw_b + cb + wcol : kOob), 0, kCpolX2));
+    }
+    load_x(c, b.x);
+  };
+  f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  auto mma = [&](const Batch& b) __attribute__((always_inline)) {
+    const V* x = b.x;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i)
+      *reinterpret_cast<V*>(area + (i * RPI + wrow) * PITCH + wcol) = b.w[i];
+#pragma unroll
+    for (int t = 0; t < KG; ++t) {
+      const V a = *reinterpret_cast<const V*>(area + q * PITCH + 64 * t + 16 * g);
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t & 1] = mfma16x16x4(a[u], x[t][u], acc[t & 1]);
+      } else {
+        acc[t & 1] = mfma16x16x32bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, x[t]), acc[t & 1]);
+      }
+    }
+  };
+  const int nch = (int)((kbytes + CHB - 1) / CHB);
+  const int mine = nch > wave ? (nch - wave + WAVES - 1) / WAVES : 0;  // chunks wave, wave + WAVES, ...
+  // Ring of NB register sets: chunk j + NB - 1 is loaded before chunk j is
+  // used (loads past the last chunk are masked and touch no memory).
+  Batch ring[NB];
+#pragma unroll
+  for (int s = 0; s < NB - 1; ++s) load(wave + s * WAVES, ring[s]);
+  for (int j = 0; j < mine; j += NB) {
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      load(wave + (j + s + NB - 1) * WAVES, ring[(s + NB - 1) % NB]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + s < mine) mma(ring[s]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // Each wave parks its sum in its own area (after its own reads, in order);
+  // wave 0 adds them in wave order.  Lane l holds out[m0 + q][n0 + 4 g + v].
+  *reinterpret_cast<f32x4*>(area + 16 * lane) = acc[0] + acc[1];
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 s = *reinterpret_cast<const f32x4*>(lds + 16 * lane);
+#pragma unroll
+  for (int v = 1; v < WAVES; ++v) s += *reinterpret_cast<const f32x4*>(lds + v * 16 * PITCH + 16 * lane);
+  if (m0 + q >= M) return;
+  float* orow = out + (int64_t)(m0 + q) * ldo;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int i = 4 * g + v;
+    if (i < R && n0 + i < N) orow[n0 + i] = s[v];
+  }
+}
+
 // x @ W.T with a 16-byte aligned row-major x1 and W (K and both strides
 // multiples of the 16-byte element count), M <= MR: the row-dot kernel; any
 // other layout or alignment runs the streaming kernel's variant FB.
@@ -697,6 +833,24 @@ hipError_t launch_rows(const MatmulArgs& a, FB fallback) {
 template <typename T, int MR, int RPW, int WAVES, int U>
 hipError_t launch_rows_or_skinny(const MatmulArgs& a) {
   return launch_rows<T, MR, RPW, WAVES, U, kCpolX2>(a, [](const MatmulArgs& b) { return launch_skinny<T, 4, 2>(b); });
+}
+
+// x @ W.T with M <= 16 under the same layout and alignment conditions: the
+// row-tile kernel; anything else runs skinny_*_w4_b2.  Byte offsets within
+// the 16 rows of x1 and of W a workgroup reads must fit 31 bits.
+template <typename T, int WAVES, int CHB, int R, int NB>
+hipError_t launch_wt_or_skinny(const MatmulArgs& a) {
+  constexpr int EPL = 16 / (int)sizeof(T);
+  auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const int64_t esz = (int64_t)sizeof(T), lim = (int64_t(1) << 31) - 2 * CHB;
+  const bool fits = (a.layout & 3) == TILEC_X2_COL_MAJOR && a.M <= 16 && a.K % EPL == 0 && a.ldx1 % EPL == 0 &&
+                    a.ldx2 % EPL == 0 && aligned(a.x1) && aligned(a.x2) && 15 * a.ldx1 * esz + a.K * esz < lim &&
+                    (R - 1) * a.ldx2 * esz + a.K * esz < lim;
+  if (!fits) return launch_skinny<T, 4, 2>(a);
+  hipLaunchKernelGGL((gemv_wt_kernel<T, WAVES, CHB, R, NB>), dim3((unsigned)cdiv(a.N, R), (unsigned)cdiv(a.M, 16)),
+                     dim3(WAVES * 64), 0, a.stream, static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out,
+                     (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -732,6 +886,15 @@ const VariantDesc* skinny_variants(int* count) {
       {"skinny_bf16_t1_r1_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 4, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 1, 4, 4>},
       {"skinny_bf16_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 2, 4, 4>},
       {"skinny_bf16_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<u16, 4, 2, 4, 2>},
+      // x @ W.T, M <= 16: row-tile kernel, 16 rows of W per workgroup over all of K (BN), K chunks of
+      // 1 KiB (c1k) or 512 bytes (c512) per row, a ring of 2 register sets (1 for the 16-wave
+      // variant, whose 4 waves per SIMD leave 128 registers each); other layouts run skinny_*_w4_b2.
+      {"skinny_f32_t16_r16_w8_c512", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 2, launch_wt_or_skinny<float, 8, 512, 16, 2>},
+      {"skinny_f32_t16_r16_w16_c512", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 16, 16, 1, launch_wt_or_skinny<float, 16, 512, 16, 1>},
+      {"skinny_f32_t16_r16_w4_c1k", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 4, 16, 2, launch_wt_or_skinny<float, 4, 1024, 16, 2>},
+      {"skinny_bf16_t16_r16_w8_c512", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 2, launch_wt_or_skinny<u16, 8, 512, 16, 2>},
+      {"skinny_bf16_t16_r16_w16_c512", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 16, 16, 1, launch_wt_or_skinny<u16, 16, 512, 16, 1>},
+      {"skinny_bf16_t16_r16_w4_c1k", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 4, 16, 2, launch_wt_or_skinny<u16, 4, 1024, 16, 2>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

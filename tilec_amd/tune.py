@@ -217,12 +217,13 @@ def _draw(rng):
     return None
 
 
-def shapes(n=500, seed=0, n_layout=120, n_rows=40):
+def shapes(n=500, seed=0, n_layout=120, n_rows=40, n_tile=30):
     """Seeded random shapes (M, K, N, dtype, layout): `n` row-major draws plus
     CONFIG_SHAPES, `n_layout` draws of a second stream (seed + 1) with a
-    random non-row-major layout, plus LAYOUT_CONFIG_SHAPES, and `n_rows`
-    x @ W.T shapes with M <= 4 from a third stream (seed + 2), the row-dot
-    kernel's domain."""
+    random non-row-major layout, plus LAYOUT_CONFIG_SHAPES, `n_rows` x @ W.T
+    shapes with M <= 4 from a third stream (seed + 2), the row-dot kernel's
+    domain, and `n_tile` x @ W.T shapes with 5 <= M <= 16 from a fourth
+    (seed + 3), the row-tile kernel's."""
     rng = random.Random(seed)
     out = set(CONFIG_SHAPES)
     while len(out) < n + len(CONFIG_SHAPES):
@@ -236,16 +237,20 @@ def shapes(n=500, seed=0, n_layout=120, n_rows=40):
         d = _draw(rng2)
         if d is not None:
             lay.add(d + (rng2.choice((1, 2, 2, 3)),))  # x @ W.T (x2 column-major) twice as often
-    rng3 = random.Random(seed + 2)
-    rows = set()
-    while len(rows) < n_rows:
-        M, K, N = rng3.randint(1, 4), round(2 ** rng3.uniform(8, 14)), round(2 ** rng3.uniform(8, 14))
-        if rng3.random() < 0.5:
-            K = 1 << round(math.log2(K))
-        dtype = rng3.choice(("f32", "bf16"))
-        if K * N <= 1 << 26:
-            rows.add((M, K, N, dtype, _lib.X2_COL_MAJOR))
-    return sorted(out | lay | rows, key=lambda s: (s[0] * s[1] * s[2], s))
+    def wt_stream(rng, count, m_lo, m_hi):
+        got = set()
+        while len(got) < count:
+            M, K, N = rng.randint(m_lo, m_hi), round(2 ** rng.uniform(8, 14)), round(2 ** rng.uniform(8, 14))
+            if rng.random() < 0.5:
+                K = 1 << round(math.log2(K))
+            dtype = rng.choice(("f32", "bf16"))
+            if K * N <= 1 << 26:
+                got.add((M, K, N, dtype, _lib.X2_COL_MAJOR))
+        return got
+
+    rows = wt_stream(random.Random(seed + 2), n_rows, 1, 4)
+    tile = wt_stream(random.Random(seed + 3), n_tile, 5, 16)
+    return sorted(out | lay | rows | tile, key=lambda s: (s[0] * s[1] * s[2], s))
 
 
 def operands(M, K, N, dtype, layout, gen):
