@@ -137,7 +137,7 @@ def test_row_dot_configs_only_where_the_kernel_runs():
     assert not rows(ext.hip_configs(1, 4094, 4096, "f32", _lib.X2_COL_MAJOR))
     assert not rows(ext.hip_configs(1, 4092, 4096, "bf16", _lib.X2_COL_MAJOR))
     m5 = rows(ext.hip_configs(5, 4096, 4096, "f32", _lib.X2_COL_MAJOR))
-    assert m5 and all(c.endswith(("_c1k", "_c512")) for c, _ in m5)  # only the row-tile kernel above M = 4
+    assert m5 and all(c.endswith(("_c128", "_c256")) for c, _ in m5)  # only the row-tile kernel above M = 4
     assert rows(ext.hip_configs(16, 4096, 4096, "bf16", _lib.X2_COL_MAJOR))
     assert not rows(ext.hip_configs(17, 4096, 4096, "f32", _lib.X2_COL_MAJOR))  # M above every bound
 

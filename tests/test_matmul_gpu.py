@@ -207,7 +207,7 @@ def test_skinny_fma_path():
     integers bit-exact."""
     # (the row-tile variants for x @ W.T, M <= 16, are covered by test_gemv_rows_kernel)
     fma = [v for v in _lib.variants() if v["family"] == _lib.FAMILY_SKINNY and v["max_m"]
-           and not v["name"].endswith(("_c512", "_c1k"))]
+           and not v["name"].endswith(("_c128", "_c256"))]
     assert len(fma) == 14  # 8 streaming FMA variants, 6 row-dot variants for x @ W.T
     for v in fma:
         bf = v["dtype"] == _lib.BF16
@@ -671,7 +671,7 @@ def test_graph_capture_row_dot_and_bf16_rings():
     dx, dw, dx12 = dev(x), dev(w), dev(x12)
     da, db = dev_bf16(a16), dev_bf16(b16)
     cfg_rows, cfg_ring = ("skinny_f32_t1_r1_w4", 1), ("gemm_bf16_256x256x32_r4w8", 1)
-    cfg_tile = ("skinny_f32_t16_r16_w16_c512", 1)
+    cfg_tile = ("skinny_f32_t16_r16_w8_c128", 1)
     eager = ext.matrix_mul(dx, dw.t(), cfg_rows)
     eager2 = ext.matrix_mul(da, db, cfg_ring)
     eager3 = ext.matrix_mul(dx12, dw.t(), cfg_tile)

@@ -704,9 +704,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
 // operands, so NaN padding past K cannot leak in).  Rows of the LDS area past
 // R are never written; they only feed D rows that are not stored.  A ring of
 // NB register sets keeps the loads of NB - 1 chunks in flight while a chunk
-// is multiplied (NB = 1: none; the 16-wave variants rely on their 4 waves per
-// SIMD instead).  Summing the waves in a fixed order keeps results
-// independent of scheduling.
+// is multiplied.  Small chunks (128 or 256 bytes per row: 8 or 4 rows of W
+// per wave load) and many waves keep each wave's MFMA work per chunk short,
+// so the last chunks to arrive are multiplied quickly; 512-byte and 1 KiB
+// chunks left fp32 launches waiting on MFMAs after their data had arrived.
+// Summing the waves in a fixed order keeps results independent of
+// scheduling.
 // ---------------------------------------------------------------------------
 template <typename T, int WAVES, int CHB, int R, int NB>
 __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict__ x1, const T* __restrict__ w,
@@ -717,7 +720,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
   constexpr int NLD = R / RPI;     // W wave loads per chunk
   constexpr int KG = CHB / 64;     // 64-byte k groups per chunk
   constexpr int PITCH = CHB + 16;  // LDS bytes per staged row
-  static_assert(CHB == 512 || CHB == 1024, "chunk of 512 or 1024 bytes per row");
+  static_assert(CHB == 128 || CHB == 256 || CHB == 512 || CHB == 1024, "chunk of 128 to 1024 bytes per row");
   static_assert(R <= 16 && R % RPI == 0, "R rows of W, whole wave loads");
   typedef std::conditional_t<sizeof(T) == 4, f32x4, i32x4> V;
   __shared__ __attribute__((aligned(16))) unsigned char lds[WAVES * 16 * PITCH];
@@ -887,14 +890,13 @@ const VariantDesc* skinny_variants(int* count) {
       {"skinny_bf16_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 2, 4, 4>},
       {"skinny_bf16_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<u16, 4, 2, 4, 2>},
       // x @ W.T, M <= 16: row-tile kernel, 16 rows of W per workgroup over all of K (BN), K chunks of
-      // 1 KiB (c1k) or 512 bytes (c512) per row, a ring of 2 register sets (1 for the 16-wave
-      // variant, whose 4 waves per SIMD leave 128 registers each); other layouts run skinny_*_w4_b2.
-      {"skinny_f32_t16_r16_w8_c512", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 2, launch_wt_or_skinny<float, 8, 512, 16, 2>},
-      {"skinny_f32_t16_r16_w16_c512", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 16, 16, 1, launch_wt_or_skinny<float, 16, 512, 16, 1>},
-      {"skinny_f32_t16_r16_w4_c1k", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 4, 16, 2, launch_wt_or_skinny<float, 4, 1024, 16, 2>},
-      {"skinny_bf16_t16_r16_w8_c512", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 2, launch_wt_or_skinny<u16, 8, 512, 16, 2>},
-      {"skinny_bf16_t16_r16_w16_c512", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 16, 16, 1, launch_wt_or_skinny<u16, 16, 512, 16, 1>},
-      {"skinny_bf16_t16_r16_w4_c1k", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 4, 16, 2, launch_wt_or_skinny<u16, 4, 1024, 16, 2>},
+      // 128 or 256 bytes per row, a ring of 4 register sets; other layouts run skinny_*_w4_b2.
+      {"skinny_f32_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<float, 16, 128, 16, 4>},
+      {"skinny_f32_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<float, 8, 128, 16, 4>},
+      {"skinny_f32_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<float, 8, 256, 16, 4>},
+      {"skinny_bf16_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<u16, 16, 128, 16, 4>},
+      {"skinny_bf16_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<u16, 8, 128, 16, 4>},
+      {"skinny_bf16_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<u16, 8, 256, 16, 4>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

@@ -110,24 +110,21 @@ size_t gemm_counter_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K,
 
 // Built-in rule (used when the caller passes TILEC_VARIANT_AUTO).
 int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2, int layout) {
-  // x @ W.T with M <= 16: the row-dot kernel (fp32 M <= 4, bf16 M = 1) or
-  // the row-tile kernel (no K split; both run the streaming kernel
-  // themselves when the operands are not 16-byte aligned).  Their workspace
-  // and counter needs (those of that fallback, at the split auto_split gives
-  // them, which is never above the streaming variant's) never exceed those
-  // of the streaming variant chosen below for the same shape in another
-  // layout, so sizes queried with TILEC_VARIANT_AUTO still suffice.
+  // x @ W.T with M <= 16: the row-dot kernel for M = 1, the row-tile kernel
+  // above (no K split; both run the streaming kernel themselves when the
+  // operands are not 16-byte aligned).  Their workspace and counter needs
+  // (those of that fallback, at the split auto_split gives them, which is
+  // never above the streaming variant's) never exceed those of the streaming
+  // variant chosen below for the same shape in another layout, so sizes
+  // queried with TILEC_VARIANT_AUTO still suffice.
   const int64_t epl = dtype == TILEC_F32 ? 4 : 8;  // elements per 16-byte load
   if ((layout & 3) == TILEC_X2_COL_MAJOR && M >= 1 && M <= 16 && K % epl == 0 && ldx1 % epl == 0 &&
       ldx2 % epl == 0 && skinny_fits(ldx1, ldx2, layout)) {
-    if (dtype == TILEC_F32) {
-      if (M <= 4) return find(M == 1 ? "skinny_f32_t1_r1_w4" : "skinny_f32_t4_r2_w4");
-      // one workgroup per 16 rows of W: with fewer than half the CUs busy
-      // and a long K, the streaming kernel's K split (below) is faster
-      if (cdiv(N, 16) >= kCUs / 2 || K <= 2048) return find("skinny_f32_t16_r16_w16_c512");
-    } else {
-      return find(M == 1 ? "skinny_bf16_t1_r2_w4" : "skinny_bf16_t16_r16_w16_c512");
-    }
+    if (M == 1) return find(dtype == TILEC_F32 ? "skinny_f32_t1_r1_w4" : "skinny_bf16_t1_r2_w4");
+    // one workgroup per 16 rows of W: with fewer than half the CUs busy
+    // and a long K, the streaming kernel's K split (below) is faster
+    if (cdiv(N, 16) >= kCUs / 2 || K <= 2048)
+      return find(dtype == TILEC_F32 ? "skinny_f32_t16_r16_w8_c128" : "skinny_bf16_t16_r16_w8_c128");
   }
   if (dtype == TILEC_F32) {
     if ((M <= 16 || small_output(M, N)) && cdiv(M, 16) <= kSkinnyMaxRowBlocks && skinny_fits(ldx1, ldx2, layout))

@@ -132,8 +132,8 @@ SPLIT_MAX_ACC_PER_THREAD = 64  # tilec_amd/csrc/common.h, kSplitMaxAccPerThread
 def rows_variant(v):
     """Variants named *_t<MR>_r<R>_* run a kernel for x @ W.T over all of K,
     with no K split (csrc/skinny.hip): the row-dot kernel (gemv_rows_kernel,
-    one wave per 1-2 rows of W, M <= 4) or the row-tile kernel (*_c1k /
-    *_c512: gemv_wt_kernel, R rows of W per workgroup, M <= 16); other
+    one wave per 1-2 rows of W, M <= 4) or the row-tile kernel (*_c128 /
+    *_c256: gemv_wt_kernel, 16 rows of W per workgroup, M <= 16); other
     layouts run the streaming kernel."""
     return re.search(r"_t\d+_r\d+_", v["name"]) is not None
 
