@@ -45,8 +45,10 @@
 // Grid: x = slabs of 16*CPL columns, y = K splits, z = 16-row blocks of x1
 // and out.
 //
-// x @ W.T with M <= 4 has a second kernel below, gemv_rows_kernel: one wave
-// per row of W over all of K, no K split.
+// x @ W.T with M <= 16 has two more kernels below, neither with a K split:
+// gemv_rows_kernel (one wave per row of W over all of K, FMAs, M <= 4) and
+// gemv_wt_kernel (16 rows of W per workgroup over all of K, MFMAs fed
+// through LDS).
 // Waves are summed through LDS; with a split K each workgroup writes its
 // [16 x SLAB] partial to the workspace, and the last workgroup of a (row
 // block, slab) to finish (completion counter) adds the partials in split
