@@ -208,7 +208,7 @@ def test_skinny_fma_path():
     # (the row-tile variants for x @ W.T, M <= 16, are covered by test_gemv_rows_kernel)
     fma = [v for v in _lib.variants() if v["family"] == _lib.FAMILY_SKINNY and v["max_m"]
            and not v["name"].endswith(("_c128", "_c256"))]
-    assert len(fma) == 14  # 8 streaming FMA variants, 6 row-dot variants for x @ W.T
+    assert len(fma) == 16  # 8 streaming FMA variants, 8 row-dot variants for x @ W.T
     for v in fma:
         bf = v["dtype"] == _lib.BF16
         for m in range(1, v["max_m"] + 1):
@@ -535,7 +535,7 @@ def test_gemv_rows_kernel():
     (both are masked at K, so it must not leak), against the fp64 oracle;
     small integers bit-exact; other layouts run the streaming kernel."""
     rows = [v for v in _lib.variants() if ext.rows_variant(v)]
-    assert len(rows) == 12
+    assert len(rows) == 14
     for v in rows:
         bf = v["dtype"] == _lib.BF16
         ms = range(1, v["max_m"] + 1) if v["max_m"] <= 4 else (1, 2, 5, 8, 13, 16)
@@ -670,7 +670,7 @@ def test_graph_capture_row_dot_and_bf16_rings():
     a16, b16 = O.bf16_round(O.normal((512, 1024), 72)), O.bf16_round(O.normal((1024, 512), 73))
     dx, dw, dx12 = dev(x), dev(w), dev(x12)
     da, db = dev_bf16(a16), dev_bf16(b16)
-    cfg_rows, cfg_ring = ("skinny_f32_t1_r1_w4", 1), ("gemm_bf16_256x256x32_r4w8", 1)
+    cfg_rows, cfg_ring = ("skinny_f32_t1_r1_w8_u2", 1), ("gemm_bf16_256x256x32_r4w8", 1)
     cfg_tile = ("skinny_f32_t16_r16_w8_c128", 1)
     eager = ext.matrix_mul(dx, dw.t(), cfg_rows)
     eager2 = ext.matrix_mul(da, db, cfg_ring)

@@ -891,6 +891,9 @@ const VariantDesc* skinny_variants(int* count) {
       {"skinny_bf16_t1_r1_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 4, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 1, 4, 4>},
       {"skinny_bf16_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 2, 4, 4>},
       {"skinny_bf16_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<u16, 4, 2, 4, 2>},
+      // M = 1 with 8 waves per workgroup and batches of 2 chunks (the built-in choice for M = 1).
+      {"skinny_f32_t1_r1_w8_u2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 8, 1, 2, launch_rows_or_skinny<float, 1, 1, 8, 2>},
+      {"skinny_bf16_t1_r1_w8_u2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 8, 1, 2, launch_rows_or_skinny<u16, 1, 1, 8, 2>},
       // x @ W.T, M <= 16: row-tile kernel, 16 rows of W per workgroup over all of K (BN), K chunks of
       // 128 or 256 bytes per row, a ring of 4 register sets; other layouts run skinny_*_w4_b2.
       {"skinny_f32_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<float, 16, 128, 16, 4>},

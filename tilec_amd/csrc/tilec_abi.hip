@@ -120,7 +120,7 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
   const int64_t epl = dtype == TILEC_F32 ? 4 : 8;  // elements per 16-byte load
   if ((layout & 3) == TILEC_X2_COL_MAJOR && M >= 1 && M <= 16 && K % epl == 0 && ldx1 % epl == 0 &&
       ldx2 % epl == 0 && skinny_fits(ldx1, ldx2, layout)) {
-    if (M == 1) return find(dtype == TILEC_F32 ? "skinny_f32_t1_r1_w4" : "skinny_bf16_t1_r2_w4");
+    if (M == 1) return find(dtype == TILEC_F32 ? "skinny_f32_t1_r1_w8_u2" : "skinny_bf16_t1_r1_w8_u2");
     // one workgroup per 16 rows of W: with fewer than half the CUs busy
     // and a long K, the streaming kernel's K split (below) is faster
     if (cdiv(N, 16) >= kCUs / 2 || K <= 2048)
