@@ -769,7 +769,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
   };
   f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   auto mma = [&](const Batch& b) __attribute__((always_inline)) {
-    const V* x = b.x;
 #pragma unroll
     for (int i = 0; i < NLD; ++i)
       *reinterpret_cast<V*>(area + (i * RPI + wrow) * PITCH + wcol) = b.w[i];
@@ -778,9 +777,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
       const V a = *reinterpret_cast<const V*>(area + q * PITCH + 64 * t + 16 * g);
       if constexpr (sizeof(T) == 4) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t & 1] = mfma16x16x4(a[u], x[t][u], acc[t & 1]);
+        for (int u = 0; u < 4; ++u) acc[t & 1] = mfma16x16x4(a[u], b.x[t][u], acc[t & 1]);
       } else {
-        acc[t & 1] = mfma16x16x32bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, x[t]), acc[t & 1]);
+        acc[t & 1] = mfma16x16x32bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b.x[t]), acc[t & 1]);
       }
     }
   };
