@@ -206,9 +206,10 @@ def test_skinny_fma_path():
     N, row- and column-major x1, split K, against the fp64 oracle; small
     integers bit-exact."""
     # (the row-tile variants for x @ W.T, M <= 16, are covered by test_gemv_rows_kernel)
-    fma = [v for v in _lib.variants() if v["family"] == _lib.FAMILY_SKINNY and v["max_m"]
+    fma = [v for v in _lib.variants() if v["family"] == _lib.FAMILY_SKINNY and v["max_m"] in (1, 4)
            and not v["name"].endswith(("_c128", "_c256"))]
-    assert len(fma) == 16  # 8 streaming FMA variants, 8 row-dot variants for x @ W.T
+    # 8 streaming FMA variants, 8 row-dot variants for x @ W.T, 6 panel variants
+    assert len(fma) == 22
     for v in fma:
         bf = v["dtype"] == _lib.BF16
         for m in range(1, v["max_m"] + 1):
@@ -234,6 +235,72 @@ def test_skinny_fma_path():
             conv = (lambda x: dev(x).to(torch.bfloat16)) if v["dtype"] == _lib.BF16 else dev
             for s in (1, 5):
                 np.testing.assert_array_equal(run(conv(a), conv(b), (v["name"], s)), want)
+
+
+def panel_variants():
+    return [v for v in _lib.variants() if "_p_" in v["name"]]
+
+
+def test_panel_kernel():
+    """The panel kernel (512-byte pieces of each x2 row, M <= 4, row-major
+    x2): every M up to each variant's bound, K ragged (odd, not a multiple
+    of 16) and aligned, N a multiple of the 16-byte group with a partial last
+    panel, row- and column-major x1, unsplit and split K, against the fp64
+    oracle.  Shapes it does not take (N % group != 0) run the streaming
+    fallback and are checked the same way."""
+    pv = panel_variants()
+    assert len(pv) == 6
+    shapes = [(16, 8), (36, 136), (1004, 264), (4096, 4096), (4097, 520), (333, 1000), (100, 4), (1, 256)]
+    for v in pv:
+        bf = v["dtype"] == _lib.BF16
+        for m in range(1, v["max_m"] + 1):
+            for i, (k, n) in enumerate(shapes):
+                a, b = O.normal((m, k), 60 * m + i), O.normal((k, n), 60 * m + i + 30)
+                if bf:
+                    a, b = O.bf16_round(a), O.bf16_round(b)
+                ref = O.matmul_bf16_f64(a, b) if bf else O.matmul_f64(a, b)
+                mk = dev_bf16 if bf else dev
+                for layout in (0, _lib.X1_COL_MAJOR):
+                    for s in (1, 3, 8, 64):
+                        say(f"{v['name']} m={m} k={k} n={n} layout {layout} split {s}")
+                        got = run_layout(mk(a), mk(b), layout, (v["name"], s))
+                        assert O.rel_l2(got, ref) <= (1e-5 if bf else O.TOL_F32), (v["name"], m, k, n, layout, s)
+
+
+def test_panel_exact_and_deterministic():
+    """Small integers: every partial sum is exact in fp32, so any split and
+    summation order gives the int64 product bit for bit; a repeat call gives
+    the same bits; the counters are zero again after every call."""
+    rng = np.random.default_rng(31)
+    L = _lib.lib()
+    for m in (1, 3, 4, 9, 16):
+        a = rng.integers(-3, 4, (m, 3008)).astype(np.float32)
+        b = rng.integers(-3, 4, (3008, 392)).astype(np.float32)
+        want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+        for v in panel_variants():
+            if m > v["max_m"]:
+                continue
+            conv = (lambda x: dev(x).to(torch.bfloat16)) if v["dtype"] == _lib.BF16 else dev
+            x1, x2 = conv(a), conv(b)
+            for s in (1, 2, 7, 16):
+                say(f"{v['name']} exact m={m} split {s}")
+                got = run(x1, x2, (v["name"], s))
+                np.testing.assert_array_equal(got, want)
+                np.testing.assert_array_equal(run(x1, x2, (v["name"], s)), got)
+                stream = torch.cuda.current_stream().cuda_stream
+                cnt = ext._COUNTERS.get((x1.device.index, stream))
+                if cnt is not None:
+                    assert torch.count_nonzero(cnt).item() == 0, (v["name"], m, s)
+    # config 1 size with every panel variant, against the oracle
+    for m in (1, 4, 16):
+        a, b = O.normal((m, 4096), 900 + m), O.normal((4096, 4096), 901)
+        ref = O.matmul_f64(a, b)
+        for v in panel_variants():
+            if m > v["max_m"] or v["dtype"] != _lib.F32:
+                continue
+            for s in (0, 8, 16):
+                say(f"{v['name']} config-1 m={m} split {s}")
+                assert O.rel_l2(run(dev(a), dev(b), (v["name"], s)), ref) <= O.TOL_F32
 
 
 def test_skinny_row_blocks():

@@ -48,6 +48,11 @@ struct VariantDesc {
   // the workspace transposed (prep_workspace_bytes), then runs the tile GEMM
   // on k-contiguous operands; such variants never split K.
   int prep = 0;
+  // Scratch sizes of a split K (nullptr: the family's own rule).
+  size_t (*workspace_bytes)(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) = nullptr;
+  size_t (*counter_bytes)(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) = nullptr;
+  // Workgroups per CU an automatic split aims for (streaming family).
+  int wgs_per_cu = 2;
 };
 
 // Workspace of a prep variant: a transposed copy of x1 (M x K) and of x2
@@ -93,6 +98,17 @@ constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
 
 __device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t num_records = 0x7FFFFFFFu) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_records, kRsrcWord3);
+}
+// make_rsrc for a base and extent the caller knows to be wave-uniform: both
+// pass through readfirstlane, so the resource is built in scalar registers
+// even where the compiler cannot prove uniformity itself (a divergent-looking
+// resource makes it wrap each buffer instruction in a waterfall loop).
+__device__ __forceinline__ BufRsrc make_rsrc_uniform(const void* base, uint32_t num_records) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  const uint32_t n = (uint32_t)__builtin_amdgcn_readfirstlane((int)num_records);
+  return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo), n);
 }
 __device__ __forceinline__ float load_f32(BufRsrc r, uint32_t off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));

@@ -203,11 +203,15 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   // Resource of one operand for step k0: based at its tile's first element,
   // zero records past this workgroup's steps; an r-contiguous operand's K
   // edge (!KFULL) is the end of its (K - k0)-th stored row.
+  // Every input is wave-uniform (tile origin, K step, split range); they go
+  // through readfirstlane so the compiler keeps the resource in scalar
+  // registers: otherwise it loses track of that after the live / past-K
+  // select and wraps every direct-to-LDS copy in a waterfall loop.
   auto op_rsrc = [&](const u16* X, int64_t ld, int r0, bool kcontig, int k0, bool live) {
     const u16* base = kcontig ? X + (int64_t)r0 * ld + k0 : X + (int64_t)k0 * ld + r0;
     uint32_t recs = live ? 0x7FFFFFFFu : 0u;
     if (!KFULL && !kcontig && live) recs = (uint32_t)min<int64_t>((int64_t)(K - k0) * ld * 2, 0x7FFFFFFF);
-    return make_rsrc(base, recs);
+    return make_rsrc_uniform(base, recs);
   };
   // Instruction q (0 <= q < IPS) of step kt: A instructions first, then B.
   // (Offsets are copied out of the arrays before the builtin: passed straight

@@ -859,6 +859,19 @@ hipError_t launch_wt_or_skinny(const MatmulArgs& a) {
 
 }  // namespace
 
+// The streaming kernel as the fallback of other kernels' launchers (the
+// panel kernel, panel.hip, for layouts and alignments it does not take).
+template <typename T, int WAVES, int UB, int MV>
+hipError_t launch_skinny_fallback(const MatmulArgs& a) {
+  return launch_skinny<T, WAVES, UB, MV>(a);
+}
+template hipError_t launch_skinny_fallback<float, 4, 2, 0>(const MatmulArgs&);
+template hipError_t launch_skinny_fallback<float, 4, 2, 1>(const MatmulArgs&);
+template hipError_t launch_skinny_fallback<float, 4, 2, 4>(const MatmulArgs&);
+template hipError_t launch_skinny_fallback<u16, 4, 2, 0>(const MatmulArgs&);
+template hipError_t launch_skinny_fallback<u16, 4, 2, 1>(const MatmulArgs&);
+template hipError_t launch_skinny_fallback<u16, 4, 2, 4>(const MatmulArgs&);
+
 // Variant table for this family (its order is part of the variant numbering).
 // BM = rows per row block, BN = slab width, BK = the largest K chunk of one
 // workgroup, unroll = 16-row blocks per batch; max_m 0 = any M.

@@ -19,6 +19,7 @@ namespace tilec {
 const VariantDesc* skinny_variants(int* count);
 const VariantDesc* gemm_f32_variants(int* count);
 const VariantDesc* gemm_bf16_variants(int* count);
+const VariantDesc* panel_variants(int* count);
 size_t skinny_counter_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 size_t skinny_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 int64_t skinny_effective_splits(int64_t N, int64_t K, int split_k);
@@ -51,7 +52,7 @@ const std::vector<const VariantDesc*>& table() {
   static std::vector<const VariantDesc*> t;
   static std::once_flag once;
   std::call_once(once, [] {
-    for (auto fam : {skinny_variants, gemm_f32_variants, gemm_bf16_variants}) {
+    for (auto fam : {skinny_variants, gemm_f32_variants, gemm_bf16_variants, panel_variants}) {
       int n = 0;
       const VariantDesc* v = fam(&n);
       for (int i = 0; i < n; ++i) t.push_back(&v[i]);
@@ -68,7 +69,23 @@ int find(const char* name) {
 }
 
 constexpr int64_t kMaxDim = (int64_t(1) << 31) - 1024;  // kernels index rows/cols in int32
-constexpr int kCUs = 256;                               // MI355X compute units
+
+// Compute units of the current device (MI355X: 256; fewer in a partitioned
+// mode), read once per device; 256 if the query fails.
+int device_cus() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < kMaxDev) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (dev >= 0 && dev < kMaxDev) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
 
 // The skinny kernel addresses its operands within one block with 32-bit byte
 // offsets: row-major x2 over 16 rows (16 * ldx2 * 4 bytes < 2^31), x1 over 16
@@ -86,10 +103,10 @@ bool skinny_fits(int64_t ldx1, int64_t ldx2, int layout) {
   return ldx1 < kSkinnyMaxLdx1 && ldx2 < ((layout & TILEC_X2_COL_MAJOR) ? kSkinnyMaxLdx2ColMajor : kSkinnyMaxLdx2);
 }
 
-// Output tiles of the smallest tile GEMM (64 x 64): below kCUs of them the
+// Output tiles of the smallest tile GEMM (64 x 64): below one per CU the
 // tile GEMMs cannot fill the chip and the streaming kernel, which splits K,
 // takes the product.
-bool small_output(int64_t M, int64_t N) { return cdiv(M, 64) * cdiv(N, 64) < kCUs; }
+bool small_output(int64_t M, int64_t N) { return cdiv(M, 64) * cdiv(N, 64) < device_cus(); }
 
 // Tile-GEMM split-K partials are addressed with 32-bit byte offsets
 // (splits * tiles * BM * BN * 4 < 2^31) and splits are grid y (<= 65535).
@@ -108,8 +125,21 @@ size_t gemm_counter_bytes(const VariantDesc* d, int64_t M, int64_t N, int64_t K,
   return (size_t)gemm_tiles(d, M, N) * kSplitCounterStride * sizeof(unsigned);
 }
 
+// Scratch a variant needs for a split K.
+size_t variant_workspace_bytes(const VariantDesc* d, int dtype, int64_t M, int64_t N, int64_t K, int s) {
+  if (d->workspace_bytes) return d->workspace_bytes(*d, M, N, K, s);
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(dtype, M, N, K, s)
+                                          : gemm_workspace_bytes(d, M, N, K, s);
+}
+size_t variant_counter_bytes(const VariantDesc* d, int dtype, int64_t M, int64_t N, int64_t K, int s) {
+  if (d->counter_bytes) return d->counter_bytes(*d, M, N, K, s);
+  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(dtype, M, N, K, s)
+                                          : gemm_counter_bytes(d, M, N, K, s);
+}
+
 // Built-in rule (used when the caller passes TILEC_VARIANT_AUTO).
 int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64_t ldx2, int layout) {
+  const int cus = device_cus();
   // x @ W.T with M <= 16: the row-dot kernel for M = 1, the row-tile kernel
   // above (no K split; both run the streaming kernel themselves when the
   // operands are not 16-byte aligned).  Their workspace and counter needs
@@ -123,9 +153,15 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
     if (M == 1) return find(dtype == TILEC_F32 ? "skinny_f32_t1_r1_w8_u2" : "skinny_bf16_t1_r1_w8_u2");
     // one workgroup per 16 rows of W: with fewer than half the CUs busy
     // and a long K, the streaming kernel's K split (below) is faster
-    if (cdiv(N, 16) >= kCUs / 2 || K <= 2048)
+    if (cdiv(N, 16) >= cus / 2 || K <= 2048)
       return find(dtype == TILEC_F32 ? "skinny_f32_t16_r16_w8_c128" : "skinny_bf16_t16_r16_w8_c128");
   }
+  // Row-major x2 with M == 1: the panel kernel (512-byte row pieces, about
+  // one workgroup per CU; it runs the streaming kernel itself for operands it
+  // does not take).  Its M <= 4 variants are the tuner's to pick: at
+  // K = N = 4096 they trail the streaming kernel for 2 <= M <= 4.
+  if (!(layout & TILEC_X2_COL_MAJOR) && M == 1 && skinny_fits(ldx1, ldx2, layout))
+    return find(dtype == TILEC_F32 ? "skinny_f32_p_v1_w8" : "skinny_bf16_p_v1_w8");
   if (dtype == TILEC_F32) {
     if ((M <= 16 || small_output(M, N)) && cdiv(M, 16) <= kSkinnyMaxRowBlocks && skinny_fits(ldx1, ldx2, layout))
       return find("skinny_f32_w8_b1");
@@ -134,7 +170,7 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
     for (const char* nm : order) {
       const int v = find(nm);
       const VariantDesc* d = table()[v];
-      if (cdiv(M, d->bm) * cdiv(N, d->bn) >= kCUs) return v;
+      if (cdiv(M, d->bm) * cdiv(N, d->bn) >= cus) return v;
     }
     return find("gemm_f32_64x64x16_w2x2");
   }
@@ -145,29 +181,31 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
   for (const char* nm : order) {
     const int v = find(nm);
     const VariantDesc* d = table()[v];
-    if (cdiv(M, d->bm) * cdiv(N, d->bn) >= kCUs) return v;
+    if (cdiv(M, d->bm) * cdiv(N, d->bn) >= cus) return v;
   }
   // Few output tiles: the 128 x 128 LDS kernel, with K split to fill the chip.
   return find("gemm_bf16_128x128x64_r4");
 }
 
-// split_k == 0.  Streaming kernel: enough workgroups for ~2 per CU, while
+// split_k == 0.  Streaming kernels: enough workgroups for the variant's
+// workgroups per CU (2 for the streaming kernel, 1 for the panel kernel), while
 // every wave still gets at least one full unrolled batch of rows.  Tile
 // GEMMs: unsplit when the tiles alone fill the CUs, else about one workgroup
 // per CU, keeping at least 4 K steps per split (at most 16 splits).
 int auto_split(const VariantDesc* d, int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 1;
+  const int cus = device_cus();
   if (d->family == TILEC_FAMILY_GEMM) {
     const int64_t tiles = gemm_tiles(d, M, N);
-    if (tiles >= kCUs || d->prep || !tile_can_split(d->bm, d->bn, d->waves)) return 1;
-    int64_t s = cdiv(kCUs, tiles);
+    if (tiles >= cus || d->prep || !tile_can_split(d->bm, d->bn, d->waves)) return 1;
+    int64_t s = cdiv(cus, tiles);
     const int64_t s_max = cdiv(K, d->bk) / 4;
     if (s > s_max) s = s_max;
     if (s > 16) s = 16;
     return s < 1 ? 1 : (int)s;
   }
   const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
-  int64_t s = cdiv(2 * kCUs, cells);
+  int64_t s = cdiv((int64_t)d->wgs_per_cu * cus, cells);
   const int64_t rows_per_split_min = 16LL * d->waves;  // one 16-row block per wave
   const int64_t s_max = K / rows_per_split_min;
   if (s > s_max) s = s_max;
@@ -341,12 +379,11 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
     if (ldx2 < need2)
       return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < %s=%lld", (long long)ldx2, c2 ? "K" : "N", (long long)need2);
   }
-  const bool skinny = d->family == TILEC_FAMILY_SKINNY;
-  const size_t need = skinny ? skinny_workspace_bytes(dtype, M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
+  const size_t need = variant_workspace_bytes(d, dtype, M, N, K, s);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu workspace bytes (got %zu)", d->name, need,
                 workspace == nullptr ? (size_t)0 : workspace_bytes);
-  const size_t need_cnt = skinny ? skinny_counter_bytes(dtype, M, N, K, s) : gemm_counter_bytes(d, M, N, K, s);
+  const size_t need_cnt = variant_counter_bytes(d, dtype, M, N, K, s);
   if (need_cnt > 0 && (counters == nullptr || counter_bytes < need_cnt))
     return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu bytes of counters (got %zu)", d->name, need_cnt,
                 counters == nullptr ? (size_t)0 : counter_bytes);
@@ -379,7 +416,7 @@ size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t dty
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
   if (M == 0 || N == 0) return 0;
-  return d->family == TILEC_FAMILY_SKINNY ? skinny_workspace_bytes(dtype, M, N, K, s) : gemm_workspace_bytes(d, M, N, K, s);
+  return variant_workspace_bytes(d, dtype, M, N, K, s);
 }
 
 size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
@@ -388,7 +425,7 @@ size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype
   int s = 1;
   if (resolve(M, N, K, dtype, variant, split_k, &d, &s) != TILEC_OK) return 0;
   if (M == 0 || N == 0) return 0;
-  return d->family == TILEC_FAMILY_SKINNY ? skinny_counter_bytes(dtype, M, N, K, s) : gemm_counter_bytes(d, M, N, K, s);
+  return variant_counter_bytes(d, dtype, M, N, K, s);
 }
 
 int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {
