@@ -116,6 +116,31 @@ size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K,
                                   int32_t split_k);
 
 /*
+ * tilec_matmul without the caller's scratch: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference, whose
+ * kernel needs no scratch.  Same arguments, semantics and status codes as
+ * tilec_matmul, minus the four buffer arguments.
+ *
+ * A split K uses a static array of the library on the current device: at
+ * most 16 MiB of partial sums and 1 MiB of counters (each GPU the library
+ * runs on holds 17 MiB until the process ends).  A call that needs more
+ * (tilec_matmul_workspace_bytes / _counter_bytes) fails with
+ * TILEC_ERR_WORKSPACE before anything is enqueued; use tilec_matmul then.
+ * The first call on a device looks the array up and enqueues a small kernel
+ * that clears its counters.  Nothing is allocated.
+ *
+ * Every call on one GPU shares that GPU's array and leaves its counters at
+ * zero: calls that overlap on one GPU (concurrent streams, host threads)
+ * race and must be serialized by the caller.
+ */
+int tilec_matmul_noalloc(const void* x1, const void* x2, float* out,
+                         int64_t M, int64_t N, int64_t K,
+                         int64_t ldx1, int64_t ldx2, int64_t ldo, int32_t layout,
+                         int32_t dtype, int32_t variant, int32_t split_k,
+                         void* stream);
+
+/*
  * The variant the library's built-in rule picks for a shape (what
  * TILEC_VARIANT_AUTO runs), or a negative status.  The reference's
  * equivalent is the fixed BM=BN=64, BK=16 default of `_matrix_mul_tiled`

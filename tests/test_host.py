@@ -311,6 +311,23 @@ def test_abi_rejects_bad_arguments_before_launch():
         _lib.check(_call(variant=10 ** 6))
 
 
+def test_noalloc_rejects_oversized_scratch_before_launch():
+    # A call whose split K needs more than the static scratch fails before
+    # anything touches a device (dummy pointers, no GPU needed).
+    L = _lib.lib()
+    prep = _lib.variant_id("gemm_bf16_256x256x64_r2_kc")
+    n = 8192
+    assert L.tilec_matmul_workspace_bytes(n, n, n, _lib.BF16, prep, 1) > 16 << 20
+    rc = L.tilec_matmul_noalloc(16, 16, 16, n, n, n, n, n, n, 0, _lib.BF16, prep, 1, None)
+    assert rc == _lib.ERR_WORKSPACE
+    assert "tilec_matmul_noalloc has" in _lib.last_error()
+    # Argument errors are reported as by tilec_matmul.
+    assert L.tilec_matmul_noalloc(16, 16, 16, -1, 8, 8, 8, 8, 8, 0, 0, -1, 0, None) == _lib.ERR_VALUE
+    assert L.tilec_matmul_noalloc(16, 16, 16, 8, 8, 8, 8, 8, 8, 0, 7, -1, 0, None) == _lib.ERR_TYPE
+    # M == 0: nothing to do, no device access.
+    assert L.tilec_matmul_noalloc(None, None, None, 0, 8, 8, 8, 8, 8, 0, 0, -1, 0, None) == _lib.OK
+
+
 def test_abi_empty_outputs_enqueue_nothing():
     # M == 0 or N == 0: nothing to do, no device access (null pointers are fine).
     assert _call(M=0, x1=None, x2=None, out=None) == _lib.OK

@@ -26,6 +26,8 @@ _i64, _i32, _vp, _sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c
 SIGNATURES = {
     "tilec_matmul": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
                                     _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp]),
+    "tilec_matmul_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
+                                            _i32, _i32, _i32, _vp]),
     "tilec_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
     "tilec_matmul_counter_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
     "tilec_sum": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp]),

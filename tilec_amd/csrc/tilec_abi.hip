@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -313,6 +314,58 @@ int sum_plan(int64_t R, int64_t C, int64_t ldx, int32_t layout, int32_t dtype, i
   return TILEC_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of tilec_matmul_noalloc: one static device array per GPU, held
+// until the process ends.  Split-K partials in the first kWsMax bytes,
+// completion counters (zero at rest) in the next kCntMax.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoallocWsMax = size_t(16) << 20;
+constexpr size_t kNoallocCntMax = size_t(1) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocWsMax + kNoallocCntMax];
+
+constexpr int kMaxDevices = 64;
+std::atomic<unsigned char*> g_scratch[kMaxDevices];  // device address of `scratch` per device (set up once)
+std::mutex g_scratch_mu;
+
+__global__ void zero_words(unsigned* __restrict__ p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// Device address of `scratch` on the current device.  The first call on a
+// device looks it up (the array's name in host code is only a stand-in) and
+// clears the counter area with a fill kernel on `stream` (no memset node, so
+// a captured first call replays correctly); the device's static memory is
+// zero at load anyway.
+int scratch_of_current_device(hipStream_t stream, unsigned char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TILEC_ERR_HIP, "tilec: hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: device %d: tilec_matmul_noalloc serves devices 0..%d", dev,
+                kMaxDevices - 1);
+  unsigned char* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || addr == nullptr)
+        return fail(TILEC_ERR_HIP, "tilec: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                    hipGetErrorString(e));
+      p = static_cast<unsigned char*>(addr);
+      hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, stream, reinterpret_cast<unsigned*>(p + kNoallocWsMax),
+                         kNoallocCntMax / sizeof(unsigned));
+      e = hipGetLastError();
+      if (e != hipSuccess)
+        return fail(TILEC_ERR_HIP, "tilec: clearing the scratch counters failed: %s", hipGetErrorString(e));
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return TILEC_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -408,6 +461,27 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
   if (e != hipSuccess)
     return fail(TILEC_ERR_HIP, "tilec: launching %s failed: %s", d->name, hipGetErrorString(e));
   return TILEC_OK;
+}
+
+int tilec_matmul_noalloc(const void* x1, const void* x2, float* out, int64_t M, int64_t N, int64_t K,
+                         int64_t ldx1, int64_t ldx2, int64_t ldo, int32_t layout, int32_t dtype, int32_t variant,
+                         int32_t split_k, void* stream) {
+  g_err[0] = 0;
+  const size_t ws = tilec_matmul_workspace_bytes(M, N, K, dtype, variant, split_k);
+  const size_t cnt = tilec_matmul_counter_bytes(M, N, K, dtype, variant, split_k);
+  if (ws > kNoallocWsMax || cnt > kNoallocCntMax)
+    return fail(TILEC_ERR_WORKSPACE,
+                "tilec: this call needs %zu bytes of scratch and %zu of counters; tilec_matmul_noalloc has %zu and "
+                "%zu (use tilec_matmul with caller-owned buffers)",
+                ws, cnt, kNoallocWsMax, kNoallocCntMax);
+  unsigned char* base = nullptr;
+  if (ws > 0 || cnt > 0) {
+    const int rc = scratch_of_current_device(static_cast<hipStream_t>(stream), &base);
+    if (rc != TILEC_OK) return rc;
+  }
+  return tilec_matmul(x1, x2, out, M, N, K, ldx1, ldx2, ldo, layout, dtype, variant, split_k,
+                      base, base ? kNoallocWsMax : 0, base ? base + kNoallocWsMax : nullptr,
+                      base ? kNoallocCntMax : 0, stream);
 }
 
 size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,
