@@ -57,6 +57,8 @@ extern "C" {
 #define TILEC_FAMILY_SKINNY 0 /* output-stationary streaming kernel, split K:   */
                               /* M <= 16, or outputs of few 64x64 tiles         */
 #define TILEC_FAMILY_GEMM 1   /* LDS-staged MFMA tile GEMM                      */
+#define TILEC_FAMILY_DIRECT 2 /* fp32 MFMA on operands loaded straight into     */
+                              /* registers, split K: GEMV and small outputs     */
 
 /* Operand layouts: bits of tilec_matmul's `layout` (0 = both row-major). */
 #define TILEC_X1_COL_MAJOR 1 /* x1 element (m, k) at x1[m + k * ldx1], ldx1 >= M */

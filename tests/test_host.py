@@ -91,6 +91,10 @@ def test_hip_configs_rules():
                 assert v["max_m"] == 0 or M <= v["max_m"]
                 eff = ext._skinny_splits(K, s, v["bk"])
                 assert eff == 1 or K // eff >= 16 * v["waves"]
+            elif v["family"] == _lib.FAMILY_DIRECT:
+                eff = ext._direct_splits(K, s)
+                assert dt == "f32" and ext.skinny_regime(M, N, dt) and v["bm"] < 2 * max(M, 16)
+                assert eff == 1 or ext.cdiv(K, eff) >= 16 * v["waves"]
             else:
                 tiles = ext.cdiv(M, v["bm"]) * ext.cdiv(N, v["bn"])
                 eff = ext._gemm_splits(K, s, v["bk"])
@@ -102,6 +106,29 @@ def test_hip_configs_rules():
     assert ("gemm_bf16_128x128x64_r4", 8) in ext.hip_configs(1, 4096, 4096, "bf16")
     assert ("gemm_f32_128x64x16_w2x2", 4) in ext.hip_configs(1024, 1024, 1024, "f32")
     assert all(s == 1 for _, s in ext.hip_configs(8192, 8192, 8192, "bf16"))
+
+
+def test_direct_split_geometry_matches_the_library():
+    """Direct kernel: K chunks of a multiple of 16 rows, none empty; scratch =
+    splits * tiles * (16-byte values per thread after the waves meet) *
+    threads, counters = one 256-byte line per tile, none when unsplit."""
+    L = _lib.lib()
+    for v in [v for v in _lib.variants() if v["family"] == _lib.FAMILY_DIRECT]:
+        items = 4 * (v["bm"] // 16) * (v["bn"] // 64)
+        nv = ext.cdiv(items, v["waves"])
+        for M, N, K in [(1, 4096, 4096), (513, 127, 3001), (127, 513, 1000), (16, 64, 16), (5, 7, 1)]:
+            tiles = ext.cdiv(M, v["bm"]) * ext.cdiv(N, v["bn"])
+            for s in (1, 2, 3, 8, 16, 64, 5000):
+                eff = ext._direct_splits(K, s)
+                kc = ext.cdiv(ext.cdiv(K, s), 16) * 16
+                assert eff == ext.cdiv(K, kc) and (eff - 1) * kc < K
+                ws = L.tilec_matmul_workspace_bytes(M, N, K, _lib.F32, v["id"], s)
+                cnt = L.tilec_matmul_counter_bytes(M, N, K, _lib.F32, v["id"], s)
+                if eff == 1:
+                    assert ws == 0 and cnt == 0, (v["name"], M, N, K, s)
+                else:
+                    assert ws == eff * tiles * nv * v["waves"] * 64 * 16, (v["name"], M, N, K, s)
+                    assert cnt == tiles * 64 * 4, (v["name"], M, N, K, s)
 
 
 def test_gemm_split_geometry_matches_the_library():

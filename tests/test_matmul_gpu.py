@@ -303,6 +303,64 @@ def test_panel_exact_and_deterministic():
                 assert O.rel_l2(run(dev(a), dev(b), (v["name"], s)), ref) <= O.TOL_F32
 
 
+def direct_variants():
+    return [v for v in _lib.variants() if v["family"] == _lib.FAMILY_DIRECT]
+
+
+DIRECT_SHAPES = [(1, 4096, 4096), (4, 4096, 4096), (16, 4096, 4096), (7, 1000, 65), (16, 37, 3001),
+                 (513, 3001, 127), (127, 1000, 513), (512, 4096, 64), (100, 4097, 33), (33, 16, 1)]
+
+
+def test_direct_kernel():
+    """The direct-operand MFMA kernel (operands loaded straight into MFMA
+    registers, K split over waves and workgroups): the GEMV and small-output
+    BASELINE shapes plus ragged ones (K and N not multiples of 4, M past a
+    tile), every layout, unsplit and split K, against the fp64 oracle."""
+    dv = direct_variants()
+    assert len(dv) == 5
+    for i, (m, k, n) in enumerate(DIRECT_SHAPES):
+        a, b = O.normal((m, k), 1100 + 2 * i), O.normal((k, n), 1101 + 2 * i)
+        ref = O.matmul_f64(a, b)
+        x1, x2 = dev(a), dev(b)
+        for v in dv:
+            for layout in (0, *LAYOUTS):
+                for s in (1, 5, 16):
+                    say(f"{v['name']} {(m, k, n)} layout {layout} split {s}")
+                    got = run_layout(x1, x2, layout, (v["name"], s))
+                    assert O.rel_l2(got, ref) <= O.TOL_F32, (v["name"], (m, k, n), layout, s)
+
+
+def test_direct_exact_unaligned_and_deterministic():
+    """Small integers (every partial sum exact in fp32): any split and
+    summation order gives the int64 product bit for bit, also from operands
+    whose base is only 4-byte aligned (views at flat[1:]) and with padded
+    row strides; a repeat call gives the same bits; the counters are zero
+    again after every call."""
+    rng = np.random.default_rng(41)
+    for m, k, n in [(1, 3008, 392), (9, 777, 131), (16, 2051, 260), (70, 1500, 90), (513, 301, 127)]:
+        a = rng.integers(-3, 4, (m, k)).astype(np.float32)
+        b = rng.integers(-3, 4, (k, n)).astype(np.float32)
+        want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+        fa = torch.zeros(m * k + 1, device="cuda")
+        fa[1:] = dev(a).flatten()
+        fb = torch.zeros(k * (n + 3) + 1, device="cuda")
+        fb[1:].view(k, n + 3)[:, :n] = dev(b)
+        x1s = [dev(a), fa[1:].view(m, k)]
+        x2s = [dev(b), fb[1:].view(k, n + 3)[:, :n]]
+        assert x1s[1].data_ptr() % 16 == 4 and x2s[1].data_ptr() % 16 == 4
+        for v in direct_variants():
+            for x1, x2 in zip(x1s, x2s):
+                for s in (1, 3, 16, 64):
+                    say(f"{v['name']} exact {(m, k, n)} split {s} base %16 = {x1.data_ptr() % 16}")
+                    got = run(x1, x2, (v["name"], s))
+                    np.testing.assert_array_equal(got, want)
+                    np.testing.assert_array_equal(run(x1, x2, (v["name"], s)), got)
+                    stream = torch.cuda.current_stream().cuda_stream
+                    cnt = ext._COUNTERS.get((x1.device.index, stream))
+                    if cnt is not None:
+                        assert torch.count_nonzero(cnt).item() == 0, (v["name"], (m, k, n), s)
+
+
 def test_skinny_row_blocks():
     """M > 16 on the streaming kernel: one grid row block per 16 rows of x1,
     each with its own partial slots and counters (every skinny config the

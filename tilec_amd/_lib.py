@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(HERE, "libtilec_hip.so")
 # Status codes and enums (include/tilec.h).
 OK, ERR_VALUE, ERR_TYPE, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_HIP = 0, 1, 2, 3, 4, 5
 F32, BF16 = 0, 1
-FAMILY_SKINNY, FAMILY_GEMM = 0, 1
+FAMILY_SKINNY, FAMILY_GEMM, FAMILY_DIRECT = 0, 1, 2
 X1_COL_MAJOR, X2_COL_MAJOR = 1, 2  # layout bits
 VARIANT_AUTO = -1
 

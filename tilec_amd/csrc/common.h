@@ -209,14 +209,15 @@ __device__ __forceinline__ bool splitk_combine(f32x4 (&v)[NV], const bool (&live
 #pragma unroll
       for (int q = 0; q < NV; ++q) p[j][q] = load_f32x4_coherent(rw, load ? off(s, q) : kOob);
     }
+    // Branch-free: an exit here would let the compiler sink each load
+    // into its own guarded block and wait for them one at a time.
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int s = s0 + j;
-      if (s >= S) break;
 #pragma unroll
       for (int q = 0; q < NV; ++q) {
         const f32x4 x = s == split ? v[q] : p[j][q];
-        t[q] = s == 0 ? x : t[q] + x;
+        t[q] = s < S ? (s == 0 ? x : t[q] + x) : t[q];
       }
     }
   }

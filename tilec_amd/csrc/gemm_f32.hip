@@ -379,6 +379,14 @@ hipError_t launch_gemm_f32(const MatmulArgs& a) {
 
 }  // namespace
 
+// The 64 x 64 tile with K unsplit: the fallback of kernels whose own
+// addressing does not cover an operand's strides.
+hipError_t launch_gemm_f32_unsplit(const MatmulArgs& a) {
+  MatmulArgs b = a;
+  b.split_k = 1;
+  return launch_gemm_f32<64, 64, 16, 2, 2>(b);
+}
+
 // Variant table for this family (its order is part of the variant numbering).
 const VariantDesc* gemm_f32_variants(int* count) {
   static const VariantDesc t[] = {

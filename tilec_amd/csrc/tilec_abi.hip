@@ -21,6 +21,8 @@ const VariantDesc* skinny_variants(int* count);
 const VariantDesc* gemm_f32_variants(int* count);
 const VariantDesc* gemm_bf16_variants(int* count);
 const VariantDesc* panel_variants(int* count);
+const VariantDesc* direct_variants(int* count);
+int64_t direct_effective_splits(int64_t K, int split_k);
 size_t skinny_counter_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 size_t skinny_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 int64_t skinny_effective_splits(int64_t N, int64_t K, int split_k);
@@ -53,7 +55,7 @@ const std::vector<const VariantDesc*>& table() {
   static std::vector<const VariantDesc*> t;
   static std::once_flag once;
   std::call_once(once, [] {
-    for (auto fam : {skinny_variants, gemm_f32_variants, gemm_bf16_variants, panel_variants}) {
+    for (auto fam : {skinny_variants, gemm_f32_variants, gemm_bf16_variants, panel_variants, direct_variants}) {
       int n = 0;
       const VariantDesc* v = fam(&n);
       for (int i = 0; i < n; ++i) t.push_back(&v[i]);
@@ -205,6 +207,7 @@ int auto_split(const VariantDesc* d, int64_t M, int64_t N, int64_t K) {
     if (s > 16) s = 16;
     return s < 1 ? 1 : (int)s;
   }
+  // Streaming and direct kernels alike.
   const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
   int64_t s = cdiv((int64_t)d->wgs_per_cu * cus, cells);
   const int64_t rows_per_split_min = 16LL * d->waves;  // one 16-row block per wave
@@ -257,6 +260,17 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
     if (g.splits > 1 && (int64_t)gemm_workspace_bytes(d, M, N, K, s) > kGemmMaxPartialBytes)
       return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits of %lld tiles of partials is too many", d->name,
                   (long long)g.splits, (long long)gemm_tiles(d, M, N));
+  }
+  if (d->family == TILEC_FAMILY_DIRECT) {
+    const int64_t splits = direct_effective_splits(K, s);
+    const int64_t tiles = cdiv(N, d->bn) * cdiv(M, d->bm);
+    if (splits > 65535)
+      return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
+    if (tiles > 0x7FFFFFFF)
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld output tiles is too many", d->name, (long long)tiles);
+    if (splits > 1 && (int64_t)d->workspace_bytes(*d, M, N, K, s) >= (int64_t(1) << 31))
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits x %lld tiles of partials is too many", d->name,
+                  (long long)splits, (long long)tiles);
   }
   if (d->family == TILEC_FAMILY_SKINNY) {
     const int64_t splits = skinny_effective_splits(N, K, s);

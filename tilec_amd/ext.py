@@ -82,8 +82,10 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
     (x2 column-major, x1 row-major).  Elsewhere they run the streaming
     kernel unsplit, which is never the config to pick.
 
-    The skinny family (a K split, 16-row blocks) is offered for M <= 16 and,
-    for fp32, outputs too small to fill the chip with 64x64 tiles; the tile GEMMs
+    The skinny family (a K split, 16-row blocks) and the direct family (fp32
+    MFMAs on operands loaded straight into registers, a K split) are offered
+    for M <= 16 and, for fp32, outputs too small to fill the chip with 64x64
+    tiles; the tile GEMMs
     take any M, and K splits too when their own tiles cannot fill the CUs
     (for tiles small enough to split, at least 4 K steps per split).  This
     is the search space of tune.bench / tune.pick, as `mm_configs` is for
@@ -100,6 +102,18 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             epl = 4 if code == _lib.F32 else 8  # elements per 16-byte load
             if K % epl == 0 and (layout is None or layout == _lib.X2_COL_MAJOR):
                 out.append((v["name"], 1))  # the row-dot kernel never splits K
+        elif v["family"] == _lib.FAMILY_DIRECT:
+            # Any split that leaves every wave at least one 16-row step;
+            # no tile more than twice as tall as M needs.
+            if not skinny_regime(M, N, code) or v["bm"] >= 2 * max(M, 16):
+                continue
+            seen = set()
+            for s in _SKINNY_SPLITS:
+                eff = _direct_splits(K, s)
+                if eff in seen or (eff > 1 and cdiv(K, eff) < 16 * v["waves"]):
+                    continue
+                seen.add(eff)
+                out.append((v["name"], s))
         elif v["family"] == _lib.FAMILY_SKINNY:
             # A workgroup takes at most BK (the variant's K-slice cap) rows
             # of K, so small splits are raised; keep one entry per distinct
@@ -180,6 +194,14 @@ def _skinny_splits(K, split_k, kc_max):
         return 1
     s = max(split_k, 1, cdiv(K, kc_max))
     kc = cdiv(cdiv(K, s), 16) * 16
+    return cdiv(K, kc)
+
+
+def _direct_splits(K, split_k):
+    """Splits the direct kernel actually runs (tilec_amd/csrc/direct.hip, direct_geom)."""
+    if K <= 0:
+        return 1
+    kc = cdiv(cdiv(K, max(split_k, 1)), 16) * 16
     return cdiv(K, kc)
 
 
