@@ -1,6 +1,7 @@
 """Benchmark of tilec.ext.matrix_mul on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-ms S] [--no-cpu] [--no-extra]
+                    [--only SECTION [--case TEXT]]
 
 Prints ONE JSON line.  The headline workload is BASELINE config 2 at its
 largest size, fp32 4096^3 (the metric's "TFLOP/s + %MFMA peak at 4096^3"):
@@ -25,10 +26,14 @@ and W warmup steps.  Extra objects in the same line:
   vendor_torch_mm — the square fp32, config-4 bf16 and GEMV cases through
                  torch.mm (hipBLASLt / rocBLAS, fp32 result) on the same
                  box, data and timing protocol, for reference
-  cpu_baseline — the oracle's tiled C restatement of the reference kernel
-                 (oracle/matmul_oracle.c, OpenMP) on a bounded row sample of
-                 the same 4096^3 problem, on this box's host cores; plus
-                 torch.matmul on the CPU for the same sample
+  host_overhead — eager wall time per ext.matrix_mul call (Python, ctypes,
+                 launch) for a 1x1x1 product, a ragged small-output shape and
+                 the M=1 GEMV, next to their device time per call
+  cpu_baseline — torch.matmul on this box's host cores (every CPU the
+                 process may use), the reference's own CPU oracle: the full
+                 4096^3 product and the M=1/16 GEMVs, median of >= 5 runs
+                 after a warmup; plus (oracle_port) the oracle's tiled C
+                 restatement of the reference kernel on a row sample
 Only one GPU: --gpus above 1 exits with a message.
 """
 
@@ -55,7 +60,11 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the skinny and bf16 sections")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
-    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "vendor", "copy"],
+    p.add_argument("--case", default=None,
+                   help="with --only skinny, configs or reduce: run only the cases whose key contains this "
+                        "text (one kernel per profile run)")
+    p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "vendor", "copy",
+                                      "host", "cpu"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -111,7 +120,7 @@ def kernel_name_for(M, K, N, dtype, layout=0):
         return p
     L = _lib.lib()
     code = _lib.F32 if dtype == "f32" else _lib.BF16
-    v = L.tilec_select_variant(M, N, K, code)
+    v = L.tilec_select_variant_layout(M, N, K, code, layout, 0, 0)
     return _lib.variants()[v]["name"], L.tilec_auto_split_k(M, N, K, code, v)
 
 
@@ -157,6 +166,9 @@ def _gemv(x1, x2s, steps, mm=None, settle_ms=0.0):
     return ms * 1e3
 
 
+CASE = None  # --case filter (profiling runs)
+
+
 def _gemv_cases(ms_by_dtype, transposed, steps):
     """M x 4096 @ 4096 x 4096 per (dtype, M): x2 row-major, or (transposed)
     the column-major view W.T of a row-major weight W [N, K].  Rotating x2
@@ -171,6 +183,9 @@ def _gemv_cases(ms_by_dtype, transposed, steps):
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         esz = 4 if dtype == "f32" else 2
         nbuf = (512 << 20) // (esz * K * N)
+        Ms = [M for M in Ms if CASE is None or CASE == (f"M{M}" if dtype == "f32" else f"bf16_M{M}")]
+        if not Ms:
+            continue
         x2s = [torch.from_numpy(O.normal((K, N), 3 + 1000 * i)).to(tdt).cuda() for i in range(nbuf)]
         if transposed:  # the same values, stored as W [N, K] and passed as W.T
             x2s = [x.t().contiguous().t() for x in x2s]
@@ -182,7 +197,8 @@ def _gemv_cases(ms_by_dtype, transposed, steps):
             nbytes = esz * (M * K + K * N) + 4 * M * N
             gbs = nbytes / (us * 1e-6) / 1e9
             key = (f"M{M}" if dtype == "f32" else f"bf16_M{M}")
-            out[key] = dict(us=us, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, config=list(cfg))
+            out[key] = dict(us=us, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, config=list(cfg),
+                            traffic=traffic_of(cfg[0], M, N, K, "x2T" if transposed else ""))
             log(f"gemv {dtype} M={M}{' x @ W.T' if transposed else ''}: {us:.2f} us/launch, {gbs:.0f} GB/s ({cfg})")
         del x2s
     return out
@@ -203,11 +219,15 @@ def bench_layouts(steps=200, gemm_steps=20):
     from tilec_amd import ext
     out = {"gemv_x_WT": _gemv_cases((("f32", (1, 16)), ("bf16", (1, 16))), True, steps)}
     for dtype, n, peak in (("f32", 4096, PEAK_FP32_MFMA), ("bf16", 8192, PEAK_BF16_MFMA)):
+        if CASE is not None and not CASE.startswith(f"{dtype}_{n}"):
+            continue
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         a = torch.from_numpy(O.uniform((n, n), 4)).to(tdt).cuda()
         b = torch.from_numpy(O.uniform((n, n), 5)).to(tdt).cuda()
         at, bt = a.t().contiguous().t(), b.t().contiguous().t()  # same values, column-major
         for name, x1, x2 in (("x1T", at, b), ("x2T", a, bt), ("x1T_x2T", at, bt)):
+            if CASE is not None and CASE not in f"{dtype}_{n}_{name}":
+                continue
             cfg = kernel_name_for(n, n, n, dtype, ext.layout_of(x1, x2))
             ms = timed(lambda: ext.matrix_mul(x1, x2), gemm_steps, 3, settle_ms=SETTLE_MS)
             tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
@@ -303,6 +323,8 @@ def bench_configs(reps=20):
     from tilec_amd import ext
     out = {}
     for i, (name, M, K, N, gen) in enumerate(CONFIG_CASES):
+        if CASE is not None and CASE not in name:
+            continue
         draw = O.uniform if gen == "uniform" else O.normal
         x1 = torch.from_numpy(draw((M, K), 100 + 2 * i)).cuda()
         x2 = torch.from_numpy(draw((K, N), 101 + 2 * i)).cuda()
@@ -322,7 +344,8 @@ def bench_configs(reps=20):
             ms = timed(g.replay, 3, 1, stream=s, settle_ms=SETTLE_MS / 2) / reps
         del outs
         tflops = 2 * M * N * K / (ms * 1e-3) / 1e12
-        out[name] = dict(us=ms * 1e3, TFLOPs=tflops, frac=tflops / PEAK_FP32_MFMA, config=list(cfg))
+        out[name] = dict(us=ms * 1e3, TFLOPs=tflops, frac=tflops / PEAK_FP32_MFMA, config=list(cfg),
+                         traffic=traffic_of(cfg[0], M, N, K))
         log(f"{name}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s ({cfg})")
     return out
 
@@ -346,6 +369,8 @@ def bench_reduce(reps=8):
     from tilec_amd import ext
     out = {}
     for i, (name, R, C, dtype, axis) in enumerate(REDUCE_CASES):
+        if CASE is not None and CASE not in name:
+            continue
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
         esz = 4 if dtype == "f32" else 2
         nbuf = max(2, (512 << 20) // (esz * R * C))
@@ -368,7 +393,7 @@ def bench_reduce(reps=8):
         del outs, xs
         nbytes = esz * R * C + 4 * (R if axis == 1 else C)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        out[name] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes)
+        out[name] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, traffic=traffic_of("sum", R, C, axis))
         log(f"sum {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM:.1f}% of HBM)")
     return out
 
@@ -383,14 +408,16 @@ def bench_copy(nbytes=256 << 20, reps=10):
     return dict(bytes_each_way=nbytes, reps=reps, us=ms * 1e3, GBps=2 * nbytes / (ms * 1e-3) / 1e9)
 
 
-def traffic_of(kernel, M, N, K):
+def traffic_of(kernel, M, N, K, tag=""):
     """HBM bytes per launch measured with rocprofv3 (FETCH_SIZE + WRITE_SIZE,
     scaled by the copy calibration), as recorded in profiles/traffic.json for
-    this kernel and shape; None when it has not been measured."""
+    this kernel and shape (key kernel@MxNxK, plus /tag for a layout other
+    than row-major); None when it has not been measured.  Sums: kernel
+    "sum", M x N = R x C, K = axis."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(path) as f:
-            rec = json.load(f).get(f"{kernel}@{M}x{N}x{K}")
+            rec = json.load(f).get(f"{kernel}@{M}x{N}x{K}" + (f"/{tag}" if tag else ""))
     except (OSError, ValueError):
         return None
     return None if rec is None else rec.get("bytes")
@@ -407,47 +434,128 @@ def cpu_model():
     return platform.processor()
 
 
+def host_threads():
+    """CPU threads this process may run on (the box's share of the host)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def _median_runs(fn, min_runs=5, target_s=3.0, max_runs=50):
+    """Median wall time of fn() after one untimed warmup run: at least
+    `min_runs` runs, more while the total stays under `target_s`."""
+    fn()
+    runs = []
+    while len(runs) < min_runs or (sum(runs) < target_s and len(runs) < max_runs):
+        t = time.perf_counter()
+        fn()
+        runs.append(time.perf_counter() - t)
+    return sorted(runs)[len(runs) // 2], runs
+
+
 def bench_cpu(target_s):
-    """The oracle's tiled restatement of `_matmul_tiled` on a row sample of the
-    4096^3 problem (same seeded inputs), OpenMP over the host's cores."""
-    import numpy as np
+    """CPU baseline: torch.matmul on this box's host cores (the reference's
+    own CPU oracle, tests/test_matmul.py:39) on the same seeded inputs, all
+    threads this process may use; the full 4096^3 product and the config-1
+    GEMVs (M = 1, 16).  Also, as an extra key, the oracle's tiled C
+    restatement of `_matmul_tiled` (oracle/matmul_oracle.c, OpenMP) on a row
+    sample of the 4096^3 product."""
     import torch
     from oracle import oracle as O
     n = 4096
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
-    threads = min(threads, os.cpu_count() or threads)
-    O.set_num_threads(threads)
-    a = O.uniform((n, n), 4)
-    b = O.uniform((n, n), 5)
-    rows = 64
-    t = time.perf_counter()
-    O.matmul_tiled_f32(a[:rows], b)
-    t0 = time.perf_counter() - t
-    rows = int(min(n, max(64, 64 * round(target_s / max(t0, 1e-3)))))
-    rows = rows // 64 * 64
-    # Repeat the sample (the whole product, when it takes well under the
-    # target) until about target_s of CPU work; the median run is reported.
-    runs = []
-    while not runs or (sum(runs) < target_s and len(runs) < 25):
-        t = time.perf_counter()
-        O.matmul_tiled_f32(a[:rows], b)
-        runs.append(time.perf_counter() - t)
-    dt = sorted(runs)[len(runs) // 2]
-    tflops = 2 * rows * n * n / dt / 1e12
-    # torch.matmul on the CPU for the same sample (the reference's oracle routine)
+    threads = host_threads()
     torch.set_num_threads(threads)
-    ta, tb = torch.from_numpy(a[:rows]), torch.from_numpy(b)
-    ta @ tb
-    t = time.perf_counter()
-    ta @ tb
-    dtt = time.perf_counter() - t
-    log(f"cpu oracle: {rows} rows in {dt:.2f} s (median of {len(runs)}) -> {tflops * 1e3:.1f} GFLOP/s on {threads} threads")
-    return dict(value=tflops, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"rows 0..{rows - 1} of the fp32 4096^3 product (2*{rows}*4096*4096 flop), "
-                       f"tiled BM=BN=64 BK=16 restatement of _matmul_tiled: median of {len(runs)} runs "
-                       f"({sum(runs):.1f} s in all), {dt:.2f} s per run",
-                cpu=cpu_model(), torch_matmul_TFLOPs=2 * rows * n * n / dtt / 1e12,
-                torch_threads=torch.get_num_threads())
+    a_np, b_np = O.uniform((n, n), 4), O.uniform((n, n), 5)
+    a, b = torch.from_numpy(a_np), torch.from_numpy(b_np)
+    dt, runs = _median_runs(lambda: torch.matmul(a, b), target_s=min(target_s, 5.0))
+    tflops = 2 * n ** 3 / dt / 1e12
+    log(f"cpu torch.matmul 4096^3: {dt * 1e3:.1f} ms (median of {len(runs)}) -> {tflops:.3f} TFLOP/s "
+        f"on {threads} threads")
+    gemv = {}
+    x2 = torch.from_numpy(O.normal((n, n), 3))
+    for M in (1, 16):
+        x1 = torch.from_numpy(O.normal((M, n), 2))
+        t, r = _median_runs(lambda: torch.matmul(x1, x2), min_runs=20, target_s=1.0, max_runs=200)
+        nbytes = 4 * (M * n + n * n) + 4 * M * n
+        gemv[f"M{M}"] = dict(us=t * 1e6, GBps=nbytes / t / 1e9, runs=len(r))
+        log(f"cpu torch.matmul {M}x4096 @ 4096x4096: {t * 1e6:.0f} us, {nbytes / t / 1e9:.1f} GB/s")
+    # The oracle port, on a row sample sized to about target_s / 2 of work.
+    O.set_num_threads(threads)
+    rows = 64
+    t0 = time.perf_counter()
+    O.matmul_tiled_f32(a_np[:rows], b_np)
+    t0 = time.perf_counter() - t0
+    rows = int(min(n, max(64, 64 * round(0.5 * target_s / max(t0, 1e-3))))) // 64 * 64
+    pdt, pruns = _median_runs(lambda: O.matmul_tiled_f32(a_np[:rows], b_np), target_s=0.5 * target_s, max_runs=25)
+    port = dict(value=2 * rows * n * n / pdt / 1e12, unit="TFLOP/s", cores=threads,
+                sample=f"rows 0..{rows - 1} of the fp32 4096^3 product, tiled BM=BN=64 BK=16 restatement of "
+                       f"_matmul_tiled (oracle/matmul_oracle.c): median of {len(pruns)} runs after 1 warmup")
+    log(f"cpu oracle port: {rows} rows in {pdt:.2f} s -> {port['value'] * 1e3:.1f} GFLOP/s on {threads} threads")
+    return dict(value=tflops, unit="TFLOP/s", cores=threads, kind="reference",
+                sample=f"the full fp32 4096^3 product (same seeded U(-1,1) inputs) through torch.matmul on the "
+                       f"CPU, torch.set_num_threads({threads}) = every CPU this process may run on: median of "
+                       f"{len(runs)} runs after 1 warmup, {dt * 1e3:.1f} ms per run",
+                cpu=cpu_model(), gemv_torch_matmul=gemv, oracle_port=port)
+
+
+HOST_CASES = (
+    # (name, M, K, N): the smallest product, a ragged small-output shape and
+    # the config-1 GEMV, fp32 row-major
+    ("1x1x1", 1, 1, 1),
+    ("127x1000x513", 127, 1000, 513),
+    ("gemv_1x4096x4096", 1, 4096, 4096),
+)
+
+
+def bench_host(calls=2000):
+    """Per-call cost of the eager path, ext.matrix_mul as a caller runs it:
+    `calls` back-to-back calls from Python then one synchronize, in wall
+    time per call, against the device time per call of the same product
+    replayed from a HIP graph (what the GPU needs).  Also the host time of
+    the Python side alone (shape checks, operand analysis, config lookup and
+    output allocation, no launch)."""
+    import torch
+    from oracle import oracle as O
+    from tilec_amd import ext
+    out = {}
+    for i, (name, M, K, N) in enumerate(HOST_CASES):
+        x1 = torch.from_numpy(O.normal((M, K), 300 + i)).cuda()
+        x2 = torch.from_numpy(O.normal((K, N), 400 + i)).cuda()
+        for _ in range(50):
+            ext.matrix_mul(x1, x2)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(calls):
+            ext.matrix_mul(x1, x2)
+        torch.cuda.synchronize()
+        eager_us = (time.perf_counter() - t) / calls * 1e6
+        # Python side only: everything matrix_mul does before the library call.
+        t = time.perf_counter()
+        for _ in range(calls):
+            M_, K_, N_ = ext._prepare(x1, x2)
+            ops = (ext._operand(x1, M_, K_), ext._operand(x2, K_, N_))
+            ext._resolve_config(None, M_, K_, N_, x1.dtype, 0)
+            torch.empty((M_, N_), dtype=torch.float32, device=x1.device)
+            torch.cuda.current_stream(x1.device).cuda_stream
+        py_us = (time.perf_counter() - t) / calls * 1e6
+        reps = 20
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            ext.matrix_mul(x1, x2)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                outs = [ext.matrix_mul(x1, x2) for _ in range(reps)]
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            dev_us = timed(g.replay, 20, 2, stream=s) / reps * 1e3
+        del outs
+        out[name] = dict(eager_us_per_call=eager_us, python_us_per_call=py_us, device_us_per_call=dev_us,
+                         calls=calls, config=list(kernel_name_for(M, K, N, "f32")))
+        log(f"host {name}: eager {eager_us:.2f} us/call (python side {py_us:.2f}), device {dev_us:.2f} us/call")
+    return out
 
 
 def main():
@@ -465,10 +573,13 @@ def main():
     _lib.lib()  # fail loudly if the HIP library is missing
     props = torch.cuda.get_device_properties(0)
 
+    global CASE
+    CASE = args.case
     if args.only:
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
                "configs": bench_configs, "layouts": bench_layouts, "reduce": bench_reduce,
-               "vendor": bench_vendor, "copy": bench_copy}[args.only]()
+               "vendor": bench_vendor, "copy": bench_copy, "host": bench_host,
+               "cpu": lambda: bench_cpu(args.cpu_seconds)}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return
 
@@ -480,6 +591,7 @@ def main():
         extra["configs"] = bench_configs()
         extra["layouts"] = bench_layouts()
         extra["reduce"] = bench_reduce()
+        extra["host_overhead"] = bench_host()
         extra["vendor_torch_mm"] = bench_vendor()
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
 

@@ -143,14 +143,24 @@ int tilec_matmul_noalloc(const void* x1, const void* x2, float* out,
                          void* stream);
 
 /*
- * The variant the library's built-in rule picks for a shape (what
- * TILEC_VARIANT_AUTO runs), or a negative status.  The reference's
- * equivalent is the fixed BM=BN=64, BK=16 default of `_matrix_mul_tiled`
- * (tilec/ext.py:54); the trained per-shape choice lives host-side in
- * tilec_amd/tune.py, as `tune.pick` does in the reference
- * (tilec/tune.py:143-151).
+ * The variant the library's built-in rule picks for a shape with both
+ * operands row-major and contiguous (what TILEC_VARIANT_AUTO runs for layout
+ * 0), or a negative status.  The reference's equivalent is the fixed
+ * BM=BN=64, BK=16 default of `_matrix_mul_tiled` (tilec/ext.py:54); the
+ * trained per-shape choice lives host-side in tilec_amd/tune.py, as
+ * `tune.pick` does in the reference (tilec/tune.py:143-151).
  */
 int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype);
+
+/*
+ * The same for any layout and strides (ldx1 / ldx2 <= 0: contiguous): what
+ * TILEC_VARIANT_AUTO runs for tilec_matmul with these arguments (x @ W.T,
+ * for instance, takes the row-dot or row-tile kernels).  No counterpart in
+ * the reference, whose operands are always made contiguous
+ * (tilec/ext.py:59-60).
+ */
+int32_t tilec_select_variant_layout(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t layout,
+                                    int64_t ldx1, int64_t ldx2);
 
 /* The split_k that split_k == 0 resolves to for this variant and shape. */
 int32_t tilec_auto_split_k(int64_t M, int64_t N, int64_t K, int32_t dtype,

@@ -398,6 +398,14 @@ def test_select_variant_rules():
     assert names[L.tilec_select_variant(4, 4096, 4096, 1)].startswith("skinny_bf16")
     assert names[L.tilec_select_variant(17, 4096, 4096, 1)].startswith("gemm_bf16")
     assert L.tilec_select_variant(4, 4, 4, 5) == -_lib.ERR_TYPE
+    # layout-aware: x @ W.T takes the row-dot (M = 1) / row-tile kernels
+    wt = _lib.X2_COL_MAJOR
+    assert names[L.tilec_select_variant_layout(1, 4096, 4096, 0, wt, 0, 0)] == "skinny_f32_t1_r1_w8_u2"
+    assert names[L.tilec_select_variant_layout(16, 4096, 4096, 1, wt, 0, 0)] == "skinny_bf16_t16_r16_w8_c128"
+    assert L.tilec_select_variant_layout(1, 4096, 4096, 0, 0, 0, 0) == L.tilec_select_variant(1, 4096, 4096, 0)
+    # an unaligned stride: the row-dot kernel does not take it
+    assert not names[L.tilec_select_variant_layout(1, 4096, 4097, 0, wt, 0, 4099)].startswith("skinny_f32_t1")
+    assert L.tilec_select_variant_layout(4, 4, 4, 0, 8, 0, 0) == -_lib.ERR_VALUE
 
 
 def test_operand_layouts_read_in_place():

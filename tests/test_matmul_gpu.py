@@ -653,8 +653,8 @@ def test_gemv_weight_transposed(m):
 def test_gemv_rows_kernel():
     """The kernels for x @ W.T (x2 column-major: W [N, K] row-major, no K
     split): the row-dot kernel (one wave per one or two rows of W over all of
-    K, M <= 4) and the row-tile kernel (16 or 8 rows of W per workgroup, MFMAs
-    fed through LDS, M <= 16).  Many M up to the variant's bound, N ragged
+    K, M <= 4) and the row-tile kernel (16 rows of W per workgroup, 8 or 16
+    waves, MFMAs fed through LDS, M <= 16).  Many M up to the variant's bound, N ragged
     against the rows per workgroup, K a multiple of the 16-byte group but not
     of the wave chunk, row strides of W and x1 past K whose padding holds NaN
     (both are masked at K, so it must not leak), against the fp64 oracle;
@@ -700,6 +700,50 @@ def test_gemv_rows_kernel():
             for layout in (0, _lib.X1_COL_MAJOR, _lib.X1_COL_MAJOR | _lib.X2_COL_MAJOR):
                 got = run_layout(conv(a), conv(np.ascontiguousarray(w.T)), layout, (v["name"], 2))
                 np.testing.assert_array_equal(got, want)
+
+
+def test_gemv_rows_unaligned_base_and_scratch():
+    """x @ W.T through base pointers that are only 4-byte (fp32) or 2- and
+    8-byte (bf16) aligned, with K and the strides aligned: every row-dot and
+    row-tile variant, AUTO and the tuned pick then run the streaming
+    fallback, at split 1 and at the automatic split, against the fp64
+    oracle.  With aligned operands the row kernels' own path needs no
+    scratch: the C ABI accepts the call with no workspace or counters."""
+    L = _lib.lib()
+    k, n = 4096, 520
+    for bf, offsets in ((False, (1,)), (True, (1, 4))):
+        dt = torch.bfloat16 if bf else torch.float32
+        rows = [v for v in _lib.variants() if ext.rows_variant(v) and v["dtype"] == (_lib.BF16 if bf else _lib.F32)]
+        for m in (1, 4, 16):
+            a, w = O.normal((m, k), 80 + m), O.normal((n, k), 81 + m)
+            if bf:
+                a, w = O.bf16_round(a), O.bf16_round(w)
+            ref = (O.matmul_bf16_f64 if bf else O.matmul_f64)(a, np.ascontiguousarray(w.T))
+            mk = dev_bf16 if bf else dev
+            for off in offsets:
+                fa = torch.zeros(m * k + off, dtype=dt, device="cuda")
+                fa[off:] = mk(a).flatten()
+                fw = torch.zeros(n * k + off, dtype=dt, device="cuda")
+                fw[off:] = mk(w).flatten()
+                x1, x2 = fa[off:].view(m, k), fw[off:].view(n, k).t()
+                assert x1.data_ptr() % 16 != 0 and x2.data_ptr() % 16 != 0
+                cfgs = [(v["name"], s) for v in rows if m <= v["max_m"] for s in (1, 0)] + [None, "auto"]
+                for cfg in cfgs:
+                    say(f"unaligned x @ W.T {'bf16' if bf else 'f32'} m={m} offset {off} {cfg}")
+                    got = run(x1, x2, _lib.VARIANT_AUTO if cfg == "auto" else cfg)
+                    assert O.rel_l2(got, ref) <= (1e-5 if bf else O.TOL_F32), (bf, m, off, cfg)
+            # aligned operands: the row kernel itself runs, without scratch
+            dx, dw = mk(a), mk(w)
+            out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            for v in rows:
+                if m > v["max_m"]:
+                    continue
+                rc = L.tilec_matmul(dx.data_ptr(), dw.data_ptr(), out.data_ptr(), m, n, k, k, k, n,
+                                    _lib.X2_COL_MAJOR, _lib.BF16 if bf else _lib.F32, v["id"], 0,
+                                    None, 0, None, 0, torch.cuda.current_stream().cuda_stream)
+                assert rc == _lib.OK, (v["name"], _lib.last_error())
+                torch.cuda.synchronize()
+                assert O.rel_l2(out.cpu().numpy(), ref) <= (1e-5 if bf else O.TOL_F32), v["name"]
 
 
 def test_non_default_stream_and_ordering():

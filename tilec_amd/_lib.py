@@ -34,6 +34,7 @@ SIGNATURES = {
     "tilec_sum_workspace_bytes": (_sz, [_i64, _i64, _i32, _i32, _i32]),
     "tilec_sum_counter_bytes": (_sz, [_i64, _i64, _i32, _i32, _i32]),
     "tilec_select_variant": (_i32, [_i64, _i64, _i64, _i32]),
+    "tilec_select_variant_layout": (_i32, [_i64, _i64, _i64, _i32, _i32, _i64, _i64]),
     "tilec_auto_split_k": (_i32, [_i64, _i64, _i64, _i32, _i32]),
     "tilec_num_variants": (_i32, []),
     "tilec_variant_info": (ctypes.c_int, [_i32, ctypes.POINTER(_i32), ctypes.POINTER(ctypes.c_char_p)]),

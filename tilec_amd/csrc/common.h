@@ -53,6 +53,11 @@ struct VariantDesc {
   size_t (*counter_bytes)(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) = nullptr;
   // Workgroups per CU an automatic split aims for (streaming family).
   int wgs_per_cu = 2;
+  // Set for variants whose own kernel needs no split-K scratch but which run
+  // a splitting fallback for operands it does not take (the row-dot and
+  // row-tile kernels): true when a call runs the variant's own kernel.  The
+  // size queries cannot see pointers, so they stay conservative.
+  bool (*own_kernel_runs)(const MatmulArgs&) = nullptr;
 };
 
 // Workspace of a prep variant: a transposed copy of x1 (M x K) and of x2
@@ -127,6 +132,23 @@ __device__ __forceinline__ void store_f32x4_coherent(BufRsrc r, uint32_t off, f3
 }
 
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// XCDs of the current device (MI355X: 8; fewer in a partitioned mode), read
+// once per device; 8 if the query fails.
+inline int device_xcds() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 8;
+  if (dev >= 0 && dev < kMaxDev) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int x = 0;
+  if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || x <= 0) x = 8;
+  if (dev >= 0 && dev < kMaxDev) cache[dev].store(x, std::memory_order_relaxed);
+  return x;
+}
 
 // Kernels with more than 64 KiB of dynamic LDS need their limit raised once
 // per device (the attribute belongs to the kernel on the current device).
@@ -286,18 +308,19 @@ inline SplitGeom gemm_split_geom(int64_t K, int64_t BK, int split_k) {
 
 // ---------------------------------------------------------------------------
 // Workgroup id -> output tile.
-// The dispatcher hands workgroups to the 8 XCDs round-robin (id i runs on
-// XCD i % 8) and every XCD has its own L2.  First renumber ids so that each
-// XCD owns one contiguous range of "logical" ids (a bijection on [0, T) for
-// any T), then walk tiles in groups of `group_m` tile-rows so the tiles an
-// XCD runs at the same time share A row-panels and B column-panels in its L2.
+// The dispatcher hands workgroups to the device's XCDs round-robin (id i
+// runs on XCD i % xcds; MI355X has 8, a partitioned device fewer) and every
+// XCD has its own L2.  First renumber ids so that each XCD owns one
+// contiguous range of "logical" ids (a bijection on [0, T) for any T), then
+// walk tiles in groups of `group_m` tile-rows so the tiles an XCD runs at
+// the same time share A row-panels and B column-panels in its L2.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int group_m,
+__device__ __forceinline__ void tile_of(int bid, int xcds, int tiles_m, int tiles_n, int group_m,
                                         int& tm, int& tn) {
   const int T = tiles_m * tiles_n;
-  const int xcd = bid & 7;
-  const int pos = bid >> 3;
-  const int q = T >> 3, rem = T & 7;
+  const int xcd = bid % xcds;
+  const int pos = bid / xcds;
+  const int q = T / xcds, rem = T % xcds;
   const int lid = xcd * q + (xcd < rem ? xcd : rem) + pos;
   const int per_group = group_m * tiles_n;
   const int g = lid / per_group;

@@ -115,7 +115,7 @@ struct OperandBf16 {
 template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool CA, bool CB>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
     const u16* __restrict__ A, const u16* __restrict__ B, float* __restrict__ C, int M, int N, int K,
-    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
+    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int xcds, int split_steps, float* __restrict__ ws,
     unsigned* __restrict__ counters) {
   using P = GemmBf16<BM, BN, BK, WM, WN>;
   using OpA = OperandBf16<BM, BK, P::NT, !CA, VEC>;
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(
   const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
+  tile_of(blockIdx.x, xcds, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
   // K steps [kt0, kt1) of this workgroup (grid y = K splits).
@@ -224,7 +224,7 @@ hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k, grid, dim3(WM * WN * 64), lds, a.stream, static_cast<const u16*>(a.x1),
                      static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo,
-                     8, (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr, g.splits > 1 ? a.counters : nullptr);
+                     8, device_xcds(), (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr, g.splits > 1 ? a.counters : nullptr);
   return hipGetLastError();
 }
 

@@ -133,7 +133,7 @@ __device__ __forceinline__ void sched_mfma_vmem() {
 template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool KFULL, bool CA, bool CB>
 __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
     const u16* __restrict__ A, const u16* __restrict__ B, float* __restrict__ C, int M, int N, int K,
-    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
+    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int xcds, int split_steps, float* __restrict__ ws,
     unsigned* __restrict__ counters) {
   using P = LdsGemm<BM, BN, BK, NBUF, WM, WN, CA, CB>;
   using SA = typename P::SA;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
+  tile_of(blockIdx.x, xcds, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   // This workgroup's K steps: [kt0, kt0 + nk) of the cdiv(K, BK) steps
   // (grid y = K splits of split_steps steps each; one split = all of K).
@@ -442,7 +442,7 @@ hipError_t launch_gemm_bf16_lds(const MatmulArgs& a) {
                             : gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, false, CA, CB>;
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)g.splits), dim3(P::NT), 0, a.stream,
                      static_cast<const u16*>(a.x1), static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N,
-                     (int)a.K, a.ldx1, a.ldx2, a.ldo, 4, (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr,
+                     (int)a.K, a.ldx1, a.ldx2, a.ldo, 4, device_xcds(), (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr,
                      g.splits > 1 ? a.counters : nullptr);
   return hipGetLastError();
 }

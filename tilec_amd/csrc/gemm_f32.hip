@@ -207,7 +207,7 @@ struct OperandF32 {
 template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool BUF, bool CA, bool CB>
 __global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesPerSimd)) void gemm_f32_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
-    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int split_steps, float* __restrict__ ws,
+    int64_t lda, int64_t ldb, int64_t ldc, int group_m, int xcds, int split_steps, float* __restrict__ ws,
     unsigned* __restrict__ counters) {
   using P = GemmF32<BM, BN, BK, WM, WN>;
   using OpA = OperandF32<BM, BK, P::NT, !CA, VEC, BUF>;
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesP
   const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
+  tile_of(blockIdx.x, xcds, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
   // K steps [kt0, kt1) of this workgroup (grid y = K splits).
@@ -339,7 +339,7 @@ hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k, grid, dim3(WM * WN * 64), lds, a.stream, static_cast<const float*>(a.x1),
                      static_cast<const float*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo,
-                     8, (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr, g.splits > 1 ? a.counters : nullptr);
+                     8, device_xcds(), (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr, g.splits > 1 ? a.counters : nullptr);
   return hipGetLastError();
 }
 

@@ -138,13 +138,13 @@ __device__ __forceinline__ float elem(const i32x4& w, int e) {
 }
 
 // Grid: x = groups of kWaves * 64 / lpr rows, y = column splits of `chunk`
-// columns (a multiple of 64 E).
-template <typename T, bool VEC>
+// columns (a multiple of 64 E).  U: 16-byte groups in flight per lane (16
+// for long rows, whose workgroup then reads 64 KiB of x at once).
+template <typename T, bool VEC, int U>
 __global__ __launch_bounds__(kNT) void row_sum_kernel(const T* __restrict__ x, float* __restrict__ out, int R, int C,
                                                       int64_t ld, int lpr, int chunk, float* __restrict__ ws,
                                                       unsigned* __restrict__ counters) {
   constexpr int E = 16 / (int)sizeof(T);
-  constexpr int U = 4;  // groups in flight per lane
   __shared__ float red[kNT];
   __shared__ int last_flag;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -327,9 +327,12 @@ template <typename T, bool VEC>
 hipError_t launch_reduce_t(const void* x, float* out, int64_t R, int64_t C, int64_t ld, int axis, const ReduceGeom& g,
                            float* ws, unsigned* counters, hipStream_t stream) {
   const dim3 grid((unsigned)g.cells, (unsigned)g.splits);
-  if (axis == 1)
-    hipLaunchKernelGGL((row_sum_kernel<T, VEC>), grid, dim3(kNT), 0, stream, static_cast<const T*>(x), out, (int)R,
-                       (int)C, ld, g.lpr, (int)g.span, ws, counters);
+  if (axis == 1 && g.lpr == 64)
+    hipLaunchKernelGGL((row_sum_kernel<T, VEC, 16>), grid, dim3(kNT), 0, stream, static_cast<const T*>(x), out,
+                       (int)R, (int)C, ld, g.lpr, (int)g.span, ws, counters);
+  else if (axis == 1)
+    hipLaunchKernelGGL((row_sum_kernel<T, VEC, 4>), grid, dim3(kNT), 0, stream, static_cast<const T*>(x), out,
+                       (int)R, (int)C, ld, g.lpr, (int)g.span, ws, counters);
   else
     hipLaunchKernelGGL((col_sum_kernel<T, VEC>), grid, dim3(kNT), 0, stream, static_cast<const T*>(x), out, (int)R,
                        (int)C, ld, (int)g.span, ws, counters);

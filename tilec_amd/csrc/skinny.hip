@@ -819,14 +819,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
 // x @ W.T with a 16-byte aligned row-major x1 and W (K and both strides
 // multiples of the 16-byte element count), M <= MR: the row-dot kernel; any
 // other layout or alignment runs the streaming kernel's variant FB.
-template <typename T, int MR, int RPW, int WAVES, int U, int CP, typename FB>
-hipError_t launch_rows(const MatmulArgs& a, FB fallback) {
+template <typename T, int MR>
+bool rows_fit(const MatmulArgs& a) {
   constexpr int EPL = 16 / (int)sizeof(T);
   auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  const bool fits = (a.layout & 3) == TILEC_X2_COL_MAJOR && a.M <= MR && a.K % EPL == 0 && a.ldx1 % EPL == 0 &&
-                    a.ldx2 % EPL == 0 && aligned(a.x1) && aligned(a.x2) &&
-                    (int64_t)a.K * (int64_t)sizeof(T) < (int64_t(1) << 31) - 64;
-  if (!fits) return fallback(a);
+  return (a.layout & 3) == TILEC_X2_COL_MAJOR && a.M <= MR && a.K % EPL == 0 && a.ldx1 % EPL == 0 &&
+         a.ldx2 % EPL == 0 && aligned(a.x1) && aligned(a.x2) &&
+         (int64_t)a.K * (int64_t)sizeof(T) < (int64_t(1) << 31) - 64;
+}
+
+template <typename T, int MR, int RPW, int WAVES, int U, int CP, typename FB>
+hipError_t launch_rows(const MatmulArgs& a, FB fallback) {
+  if (!rows_fit<T, MR>(a)) return fallback(a);
   const int64_t rows_per_wg = (int64_t)WAVES * RPW;
   hipLaunchKernelGGL((gemv_rows_kernel<T, MR, RPW, WAVES, U, CP>), dim3((unsigned)cdiv(a.N, rows_per_wg)), dim3(WAVES * 64),
                      0, a.stream, static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out, (int)a.M, (int)a.N,
@@ -842,15 +846,19 @@ hipError_t launch_rows_or_skinny(const MatmulArgs& a) {
 // x @ W.T with M <= 16 under the same layout and alignment conditions: the
 // row-tile kernel; anything else runs skinny_*_w4_b2.  Byte offsets within
 // the 16 rows of x1 and of W a workgroup reads must fit 31 bits.
-template <typename T, int WAVES, int CHB, int R, int NB>
-hipError_t launch_wt_or_skinny(const MatmulArgs& a) {
+template <typename T, int CHB, int R>
+bool wt_fits(const MatmulArgs& a) {
   constexpr int EPL = 16 / (int)sizeof(T);
   auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   const int64_t esz = (int64_t)sizeof(T), lim = (int64_t(1) << 31) - 2 * CHB;
-  const bool fits = (a.layout & 3) == TILEC_X2_COL_MAJOR && a.M <= 16 && a.K % EPL == 0 && a.ldx1 % EPL == 0 &&
-                    a.ldx2 % EPL == 0 && aligned(a.x1) && aligned(a.x2) && 15 * a.ldx1 * esz + a.K * esz < lim &&
-                    (R - 1) * a.ldx2 * esz + a.K * esz < lim;
-  if (!fits) return launch_skinny<T, 4, 2>(a);
+  return (a.layout & 3) == TILEC_X2_COL_MAJOR && a.M <= 16 && a.K % EPL == 0 && a.ldx1 % EPL == 0 &&
+         a.ldx2 % EPL == 0 && aligned(a.x1) && aligned(a.x2) && 15 * a.ldx1 * esz + a.K * esz < lim &&
+         (R - 1) * a.ldx2 * esz + a.K * esz < lim;
+}
+
+template <typename T, int WAVES, int CHB, int R, int NB>
+hipError_t launch_wt_or_skinny(const MatmulArgs& a) {
+  if (!wt_fits<T, CHB, R>(a)) return launch_skinny<T, 4, 2>(a);
   hipLaunchKernelGGL((gemv_wt_kernel<T, WAVES, CHB, R, NB>), dim3((unsigned)cdiv(a.N, R), (unsigned)cdiv(a.M, 16)),
                      dim3(WAVES * 64), 0, a.stream, static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out,
                      (int)a.M, (int)a.N, (int)a.K, a.ldx1, a.ldx2, a.ldo);
@@ -871,6 +879,12 @@ template hipError_t launch_skinny_fallback<float, 4, 2, 4>(const MatmulArgs&);
 template hipError_t launch_skinny_fallback<u16, 4, 2, 0>(const MatmulArgs&);
 template hipError_t launch_skinny_fallback<u16, 4, 2, 1>(const MatmulArgs&);
 template hipError_t launch_skinny_fallback<u16, 4, 2, 4>(const MatmulArgs&);
+
+// A row-dot / row-tile variant: its kernel needs no scratch when `fits`.
+static VariantDesc rows_desc(VariantDesc d, bool (*fits)(const MatmulArgs&)) {
+  d.own_kernel_runs = fits;
+  return d;
+}
 
 // Variant table for this family (its order is part of the variant numbering).
 // BM = rows per row block, BN = slab width, BK = the largest K chunk of one
@@ -897,23 +911,23 @@ const VariantDesc* skinny_variants(int* count) {
       {"skinny_bf16_v4_w8_b2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, kSlabOf<u16>, kKcMax, 8, 4, 2, launch_skinny<u16, 8, 2, 4>},
       // x @ W.T (column-major x2): row-dot kernel, one or two W rows per wave, no K split (other
       // layouts run skinny_*_w4_b2).  BN = W rows per workgroup.
-      {"skinny_f32_t1_r1_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 4, kKcMax, 4, 1, 4, launch_rows_or_skinny<float, 1, 1, 4, 4>},
-      {"skinny_f32_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<float, 1, 2, 4, 4>},
-      {"skinny_f32_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<float, 4, 2, 4, 2>},
-      {"skinny_bf16_t1_r1_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 4, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 1, 4, 4>},
-      {"skinny_bf16_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 2, 4, 4>},
-      {"skinny_bf16_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<u16, 4, 2, 4, 2>},
+      rows_desc({"skinny_f32_t1_r1_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 4, kKcMax, 4, 1, 4, launch_rows_or_skinny<float, 1, 1, 4, 4>}, rows_fit<float, 1>),
+      rows_desc({"skinny_f32_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<float, 1, 2, 4, 4>}, rows_fit<float, 1>),
+      rows_desc({"skinny_f32_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<float, 4, 2, 4, 2>}, rows_fit<float, 4>),
+      rows_desc({"skinny_bf16_t1_r1_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 4, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 1, 4, 4>}, rows_fit<u16, 1>),
+      rows_desc({"skinny_bf16_t1_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 1, 4, launch_rows_or_skinny<u16, 1, 2, 4, 4>}, rows_fit<u16, 1>),
+      rows_desc({"skinny_bf16_t4_r2_w4", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 4, 4, 2, launch_rows_or_skinny<u16, 4, 2, 4, 2>}, rows_fit<u16, 4>),
       // M = 1 with 8 waves per workgroup and batches of 2 chunks (the built-in choice for M = 1).
-      {"skinny_f32_t1_r1_w8_u2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 8, 1, 2, launch_rows_or_skinny<float, 1, 1, 8, 2>},
-      {"skinny_bf16_t1_r1_w8_u2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 8, 1, 2, launch_rows_or_skinny<u16, 1, 1, 8, 2>},
+      rows_desc({"skinny_f32_t1_r1_w8_u2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 8, 1, 2, launch_rows_or_skinny<float, 1, 1, 8, 2>}, rows_fit<float, 1>),
+      rows_desc({"skinny_bf16_t1_r1_w8_u2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 8, 1, 2, launch_rows_or_skinny<u16, 1, 1, 8, 2>}, rows_fit<u16, 1>),
       // x @ W.T, M <= 16: row-tile kernel, 16 rows of W per workgroup over all of K (BN), K chunks of
       // 128 or 256 bytes per row, a ring of 4 register sets; other layouts run skinny_*_w4_b2.
-      {"skinny_f32_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<float, 16, 128, 16, 4>},
-      {"skinny_f32_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<float, 8, 128, 16, 4>},
-      {"skinny_f32_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<float, 8, 256, 16, 4>},
-      {"skinny_bf16_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<u16, 16, 128, 16, 4>},
-      {"skinny_bf16_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<u16, 8, 128, 16, 4>},
-      {"skinny_bf16_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<u16, 8, 256, 16, 4>},
+      rows_desc({"skinny_f32_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<float, 16, 128, 16, 4>}, wt_fits<float, 128, 16>),
+      rows_desc({"skinny_f32_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<float, 8, 128, 16, 4>}, wt_fits<float, 128, 16>),
+      rows_desc({"skinny_f32_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<float, 8, 256, 16, 4>}, wt_fits<float, 256, 16>),
+      rows_desc({"skinny_bf16_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<u16, 16, 128, 16, 4>}, wt_fits<u16, 128, 16>),
+      rows_desc({"skinny_bf16_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<u16, 8, 128, 16, 4>}, wt_fits<u16, 128, 16>),
+      rows_desc({"skinny_bf16_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<u16, 8, 256, 16, 4>}, wt_fits<u16, 256, 16>),
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

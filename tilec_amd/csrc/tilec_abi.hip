@@ -166,8 +166,11 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
   if (!(layout & TILEC_X2_COL_MAJOR) && M == 1 && skinny_fits(ldx1, ldx2, layout))
     return find(dtype == TILEC_F32 ? "skinny_f32_p_v1_w8" : "skinny_bf16_p_v1_w8");
   if (dtype == TILEC_F32) {
-    if ((M <= 16 || small_output(M, N)) && cdiv(M, 16) <= kSkinnyMaxRowBlocks && skinny_fits(ldx1, ldx2, layout))
-      return find("skinny_f32_w8_b1");
+    if (M <= 16 && skinny_fits(ldx1, ldx2, layout)) return find("skinny_f32_w8_b1");
+    // Few output tiles past 16 rows: the direct-operand MFMA kernel, K split
+    // across workgroups (on MI355X within 1.15x of the best measured config
+    // for such shapes, geometric mean; the streaming kernel: 1.9x).
+    if (small_output(M, N)) return find("direct_f32_32x64_w4");
     static const char* order[] = {"gemm_f32_256x256x32_w2x4", "gemm_f32_256x128x16_w2x2",
                                   "gemm_f32_128x128x32_w2x4", "gemm_f32_128x64x16_w2x2"};
     for (const char* nm : order) {
@@ -216,6 +219,16 @@ int auto_split(const VariantDesc* d, int64_t M, int64_t N, int64_t K) {
   if (s < 1) s = 1;
   if (s > 1024) s = 1024;
   return (int)s;
+}
+
+// The streaming kernel's split-K partials take 32-bit byte offsets.
+int skinny_partials_check(const VariantDesc* d, int64_t M, int64_t N, int64_t K, int s) {
+  const int64_t splits = skinny_effective_splits(N, K, s);
+  const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
+  if (splits > 1 && splits * cells * d->bm * d->bn * 4 >= (int64_t(1) << 31))
+    return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits x %lld output blocks of partials is too many",
+                d->name, (long long)splits, (long long)cells);
+  return TILEC_OK;
 }
 
 // ldx1 / ldx2 <= 0 mean "contiguous" (K and N for row-major operands, M and
@@ -273,16 +286,17 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
                   (long long)splits, (long long)tiles);
   }
   if (d->family == TILEC_FAMILY_SKINNY) {
-    const int64_t splits = skinny_effective_splits(N, K, s);
-    const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
     if (cdiv(M, d->bm) > kSkinnyMaxRowBlocks)
       return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s takes M <= %lld (got %lld)", d->name,
                   (long long)(kSkinnyMaxRowBlocks * d->bm), (long long)M);
-    if (splits > 65535)
+    if (skinny_effective_splits(N, K, s) > 65535)
       return fail(TILEC_ERR_VALUE, "tilec: split_k=%d gives more than 65535 splits", s);
-    if (splits > 1 && splits * cells * d->bm * d->bn * 4 >= (int64_t(1) << 31))
-      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: %lld splits x %lld output blocks of partials is too many",
-                  d->name, (long long)splits, (long long)cells);
+    // Row-dot / row-tile variants: checked by tilec_matmul once it knows
+    // whether their own kernel (no partials) or the streaming fallback runs.
+    if (!d->own_kernel_runs) {
+      const int rc = skinny_partials_check(d, M, N, K, s);
+      if (rc != TILEC_OK) return rc;
+    }
   }
   *out_d = d;
   *out_split = s;
@@ -446,14 +460,6 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
     if (ldx2 < need2)
       return fail(TILEC_ERR_VALUE, "tilec: ldx2=%lld < %s=%lld", (long long)ldx2, c2 ? "K" : "N", (long long)need2);
   }
-  const size_t need = variant_workspace_bytes(d, dtype, M, N, K, s);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-    return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu workspace bytes (got %zu)", d->name, need,
-                workspace == nullptr ? (size_t)0 : workspace_bytes);
-  const size_t need_cnt = variant_counter_bytes(d, dtype, M, N, K, s);
-  if (need_cnt > 0 && (counters == nullptr || counter_bytes < need_cnt))
-    return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu bytes of counters (got %zu)", d->name, need_cnt,
-                counters == nullptr ? (size_t)0 : counter_bytes);
   MatmulArgs a;
   a.x1 = x1;
   a.x2 = x2;
@@ -471,6 +477,24 @@ int tilec_matmul(const void* x1, const void* x2, float* out, int64_t M, int64_t 
   a.counters = static_cast<unsigned*>(counters);
   a.counter_bytes = counter_bytes;
   a.stream = static_cast<hipStream_t>(stream);
+  // Scratch is required only where a kernel that splits K will run: a
+  // row-dot / row-tile variant whose own kernel takes these operands needs
+  // none (the size queries, which cannot see the pointers, stay
+  // conservative).
+  if (!(d->own_kernel_runs && d->own_kernel_runs(a))) {
+    if (d->own_kernel_runs) {
+      rc = skinny_partials_check(d, M, N, K, s);
+      if (rc != TILEC_OK) return rc;
+    }
+    const size_t need = variant_workspace_bytes(d, dtype, M, N, K, s);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+      return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu workspace bytes (got %zu)", d->name, need,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    const size_t need_cnt = variant_counter_bytes(d, dtype, M, N, K, s);
+    if (need_cnt > 0 && (counters == nullptr || counter_bytes < need_cnt))
+      return fail(TILEC_ERR_WORKSPACE, "tilec: %s needs %zu bytes of counters (got %zu)", d->name, need_cnt,
+                  counters == nullptr ? (size_t)0 : counter_bytes);
+  }
   const hipError_t e = d->launch(a);
   if (e != hipSuccess)
     return fail(TILEC_ERR_HIP, "tilec: launching %s failed: %s", d->name, hipGetErrorString(e));
@@ -516,12 +540,19 @@ size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype
   return variant_counter_bytes(d, dtype, M, N, K, s);
 }
 
-int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {
+int32_t tilec_select_variant_layout(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t layout,
+                                    int64_t ldx1, int64_t ldx2) {
   const VariantDesc* d = nullptr;
   int s = 1;
-  const int rc = resolve(M, N, K, dtype, TILEC_VARIANT_AUTO, 0, &d, &s);
+  const int rc = resolve(M, N, K, dtype, TILEC_VARIANT_AUTO, 0, &d, &s, ldx1, ldx2, layout);
   if (rc != TILEC_OK) return -rc;
-  return auto_variant(M, N, K, dtype, K, N, 0);
+  if (ldx1 <= 0) ldx1 = (layout & TILEC_X1_COL_MAJOR) ? M : K;
+  if (ldx2 <= 0) ldx2 = (layout & TILEC_X2_COL_MAJOR) ? K : N;
+  return auto_variant(M, N, K, dtype, ldx1, ldx2, layout);
+}
+
+int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype) {
+  return tilec_select_variant_layout(M, N, K, dtype, 0, 0, 0);
 }
 
 int32_t tilec_auto_split_k(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant) {

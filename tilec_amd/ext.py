@@ -18,6 +18,7 @@ present.  The legacy config-space helpers of the reference (`plan`,
 """
 
 import re
+from functools import lru_cache
 
 import torch
 
@@ -98,6 +99,8 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             continue
         if v["family"] == _lib.FAMILY_SKINNY and not skinny_regime(M, N, code):
             continue
+        if panel_variant(v) and layout is not None and layout & _lib.X2_COL_MAJOR:
+            continue  # the panel kernel reads a row-major x2 (it runs the streaming kernel otherwise)
         if v["family"] == _lib.FAMILY_SKINNY and rows_variant(v):
             epl = 4 if code == _lib.F32 else 8  # elements per 16-byte load
             if K % epl == 0 and (layout is None or layout == _lib.X2_COL_MAJOR):
@@ -150,6 +153,12 @@ def rows_variant(v):
     *_c256: gemv_wt_kernel, 16 rows of W per workgroup, M <= 16); other
     layouts run the streaming kernel."""
     return re.search(r"_t\d+_r\d+_", v["name"]) is not None
+
+
+def panel_variant(v):
+    """Variants named *_p_v<M>_* run the panel kernel (csrc/panel.hip) for a
+    row-major x2 and M up to <M>."""
+    return "_p_v" in v["name"]
 
 
 def prep_variant(v):
@@ -294,36 +303,55 @@ def _prepare(x1, x2):
     return M, K, N
 
 
-def _launch(x1, x2, M, K, N, variant, split_k):
+@lru_cache(4096)
+def _scratch_sizes(M, N, K, dtype, variant, split_k):
+    """(workspace, counter) bytes a call needs; the C ABI's answer depends
+    only on these arguments, so repeat calls skip two library crossings."""
+    L = _lib.lib()
+    return (L.tilec_matmul_workspace_bytes(M, N, K, dtype, variant, split_k),
+            L.tilec_matmul_counter_bytes(M, N, K, dtype, variant, split_k))
+
+
+def _launch(x1, x2, M, K, N, variant, split_k, ops=None):
+    """Enqueue one tilec_matmul on the current stream.  `ops`: the two
+    (tensor, leading dimension, column-major?) triples of `_operand`, when
+    the caller has them already."""
     dtype = _lib.F32 if x1.dtype == torch.float32 else _lib.BF16
-    a, lda, ca = _operand(x1, M, K)
-    b, ldb, cb = _operand(x2, K, N)
+    (a, lda, ca), (b, ldb, cb) = ops or (_operand(x1, M, K), _operand(x2, K, N))
     layout = (_lib.X1_COL_MAJOR if ca else 0) | (_lib.X2_COL_MAJOR if cb else 0)
     out = torch.empty((M, N), dtype=torch.float32, device=x1.device)
     if M == 0 or N == 0:
         return out
-    L = _lib.lib()
     stream = torch.cuda.current_stream(x1.device).cuda_stream
     ws_ptr, ws_bytes, cnt_ptr, cnt_bytes = None, 0, None, 0
-    need = L.tilec_matmul_workspace_bytes(M, N, K, dtype, variant, split_k)
+    need, need_cnt = _scratch_sizes(M, N, K, dtype, variant, split_k)
     if need:
         ws = workspace_for(x1.device, stream, need)
         ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
-        cnt = counters_for(x1.device, stream, L.tilec_matmul_counter_bytes(M, N, K, dtype, variant, split_k))
+        cnt = counters_for(x1.device, stream, need_cnt)
         cnt_ptr, cnt_bytes = cnt.data_ptr(), cnt.numel()
-    _lib.check(L.tilec_matmul(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, lda, ldb, N, layout,
-                              dtype, variant, split_k, ws_ptr, ws_bytes, cnt_ptr, cnt_bytes, stream))
+    rc = _lib.lib().tilec_matmul(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, lda, ldb, N, layout,
+                                 dtype, variant, split_k, ws_ptr, ws_bytes, cnt_ptr, cnt_bytes, stream)
+    if rc:
+        _lib.check(rc)
     return out
+
+
+@lru_cache(4096)
+def _tuned(M, K, N, dtype, layout):
+    """(variant id, split_k) for the tuned pick of a shape, resolved once."""
+    from . import tune
+    config = tune.pick(M, K, N, dtype, layout)
+    if config is None:
+        return _lib.VARIANT_AUTO, 0
+    return _lib.variant_id(config[0]), int(config[1])
 
 
 def _resolve_config(config, M, K, N, dtype, layout=0):
     """config: None (tuned pick for this shape and layout), a variant name /
     id, or (variant, split_k)."""
     if config is None:
-        from . import tune
-        config = tune.pick(M, K, N, "bf16" if dtype == torch.bfloat16 else "f32", layout)
-        if config is None:
-            return _lib.VARIANT_AUTO, 0
+        return _tuned(M, K, N, "bf16" if dtype == torch.bfloat16 else "f32", layout)
     if isinstance(config, (str, int)):
         config = (config, 0)
     variant, split_k = config
@@ -344,8 +372,10 @@ def matrix_mul(x1, x2, config=None):
     (variant, split_k) from `hip_configs`.
     """
     M, K, N = _prepare(x1, x2)
-    variant, split_k = _resolve_config(config, M, K, N, x1.dtype, layout_of(x1, x2) if config is None else 0)
-    return _launch(x1, x2, M, K, N, variant, split_k)
+    ops = (_operand(x1, M, K), _operand(x2, K, N))
+    layout = (_lib.X1_COL_MAJOR if ops[0][2] else 0) | (_lib.X2_COL_MAJOR if ops[1][2] else 0)
+    variant, split_k = _resolve_config(config, M, K, N, x1.dtype, layout)
+    return _launch(x1, x2, M, K, N, variant, split_k, ops)
 
 
 def _matrix_mul_tiled(x1, x2, BM=64, BN=64, BK=16):

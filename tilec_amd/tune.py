@@ -362,9 +362,9 @@ def train(test_frac=0.2, seed=0, out=MODEL, path=None):
         best = min(r["ms"] for r in rs)
         pred = model.predict([row_features(r) for r in rs])
         chosen = rs[min(range(len(rs)), key=lambda i: pred[i])]
-        M, K, N, dtype, _ = k
+        M, K, N, dtype, layout = k
         dcode = _lib.F32 if dtype == "f32" else _lib.BF16
-        auto = _lib.variants()[L.tilec_select_variant(M, N, K, dcode)]["name"]
+        auto = _lib.variants()[L.tilec_select_variant_layout(M, N, K, dcode, layout, 0, 0)]["name"]
         auto_split = L.tilec_auto_split_k(M, N, K, dcode, _lib.variant_id(auto))
         default = [r for r in rs if r["kernel"] == auto and int(r["split_k"]) == auto_split]
         ratio_model.append(chosen["ms"] / best)
