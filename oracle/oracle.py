@@ -30,7 +30,6 @@ the invariant that row and column sums share one total.
 import ctypes
 import math
 import os
-import random
 import subprocess
 
 import numpy as np
@@ -233,21 +232,6 @@ def mm_configs(M1, N, M2):
     return [(p, r, b) for p in SPLITS for r in JOINS
             if (p == 1 or N // p >= 32) and (r == 1 or M1 >= r)
             for b in blocks(cdiv(N, p))]
-
-
-def ref_tune_shapes(n=500, seed=0):
-    """The reference tuner's shape generator, tilec/tune.py:54-65."""
-    rng = random.Random(seed)
-    out = set()
-    while len(out) < n:
-        M1 = round(2 ** rng.uniform(7, 13))
-        N = round(2 ** rng.uniform(8, 14))
-        M2 = round(2 ** rng.uniform(5, 12))
-        if rng.random() < 0.5:
-            N = 1 << round(math.log2(N))
-        if M1 * N * M2 <= 1 << 31 and M1 * N <= 1 << 25 and N * M2 <= 1 << 25:
-            out.add((M1, N, M2))
-    return sorted(out, key=lambda s: s[0] * s[1] * s[2])
 
 
 # ---------------------------------------------------------------------------

@@ -226,17 +226,6 @@ def test_mm_configs_characterisation():
         assert len(got) == len(O.mm_configs(M1, N, M2))  # no duplicates
 
 
-def test_ref_tune_shapes_properties():
-    s = O.ref_tune_shapes(200, seed=0)
-    assert len(s) == len(set(s)) == 200
-    prods = [a * b * c for a, b, c in s]
-    assert prods == sorted(prods)
-    for M1, N, M2 in s:
-        assert M1 * N * M2 <= 1 << 31 and M1 * N <= 1 << 25 and N * M2 <= 1 << 25
-        assert 2 ** 7 - 1 <= M1 <= 2 ** 13 + 1 and 2 ** 5 - 1 <= M2 <= 2 ** 12 + 1
-    assert O.ref_tune_shapes(50, seed=1) == O.ref_tune_shapes(50, seed=1)
-
-
 # ---------------------------------------------------------------------------
 # Sums (tl.sum, kernel1.py:8-15)
 # ---------------------------------------------------------------------------
