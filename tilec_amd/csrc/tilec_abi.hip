@@ -210,9 +210,13 @@ int auto_split(const VariantDesc* d, int64_t M, int64_t N, int64_t K) {
     if (s > 16) s = 16;
     return s < 1 ? 1 : (int)s;
   }
-  // Streaming and direct kernels alike.
+  // Streaming kernels: enough workgroups for the variant's workgroups per
+  // CU.  Direct kernels: at most that many, so no CU runs more chunks than
+  // the others (a grid a little over the CU count leaves a few CUs with two
+  // chunks each, and every tile then waits for them).
   const int64_t cells = cdiv(N, d->bn) * cdiv(M, d->bm);
-  int64_t s = cdiv((int64_t)d->wgs_per_cu * cus, cells);
+  int64_t s = d->family == TILEC_FAMILY_DIRECT ? (int64_t)d->wgs_per_cu * cus / cells
+                                              : cdiv((int64_t)d->wgs_per_cu * cus, cells);
   const int64_t rows_per_split_min = 16LL * d->waves;  // one 16-row block per wave
   const int64_t s_max = K / rows_per_split_min;
   if (s > s_max) s = s_max;

@@ -110,8 +110,12 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             # no tile more than twice as tall as M needs.
             if not skinny_regime(M, N, code) or v["bm"] >= 2 * max(M, 16):
                 continue
+            # Splits that fill the CUs exactly once or twice over are
+            # offered beside the powers of two.
+            tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
+            fills = [f for f in (SMALL_OUTPUT_TILES // tiles, 2 * SMALL_OUTPUT_TILES // tiles) if f > 1]
             seen = set()
-            for s in _SKINNY_SPLITS:
+            for s in sorted(set(_SKINNY_SPLITS) | set(fills)):
                 eff = _direct_splits(K, s)
                 if eff in seen or (eff > 1 and cdiv(K, eff) < 16 * v["waves"]):
                     continue
