@@ -317,7 +317,7 @@ def test_direct_kernel():
     BASELINE shapes plus ragged ones (K and N not multiples of 4, M past a
     tile), every layout, unsplit and split K, against the fp64 oracle."""
     dv = direct_variants()
-    assert len(dv) == 5
+    assert len(dv) == 7
     for i, (m, k, n) in enumerate(DIRECT_SHAPES):
         a, b = O.normal((m, k), 1100 + 2 * i), O.normal((k, n), 1101 + 2 * i)
         ref = O.matmul_f64(a, b)

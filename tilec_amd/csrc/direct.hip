@@ -336,8 +336,8 @@ int64_t direct_effective_splits(int64_t K, int split_k) { return direct_geom(1, 
 
 // Variant table of this family (appended after the earlier tables, so their
 // variant ids are unchanged).  BM x BN = the output tile, BK = the 16-row
-// step, unroll = steps per batch of loads.  The 16 x 128 tile with 8 waves is
-// the GEMV shape (x2 streamed once, one workgroup per CU); the others are
+// step, unroll = steps per batch of loads.  The 16 x 128 tile with 8 waves
+// streams x2 once (non-temporal loads, one workgroup per CU); the others are
 // for small-output GEMMs.
 const VariantDesc* direct_variants(int* count) {
   static const VariantDesc t[] = {
@@ -346,6 +346,10 @@ const VariantDesc* direct_variants(int* count) {
       direct_desc("direct_f32_32x64_w4", 2, 1, 4, 6, launch_direct<2, 1, 4, 6, false>),
       direct_desc("direct_f32_32x128_w4", 2, 2, 4, 4, launch_direct<2, 2, 4, 4, false>),
       direct_desc("direct_f32_64x64_w4", 4, 1, 4, 4, launch_direct<4, 1, 4, 4, false>),
+      // 8 waves (two per SIMD) on the small tiles: one wave's loads wait
+      // while the other's MFMAs run
+      direct_desc("direct_f32_16x64_w8", 1, 1, 8, 4, launch_direct<1, 1, 8, 4, false>),
+      direct_desc("direct_f32_32x64_w8", 2, 1, 8, 4, launch_direct<2, 1, 8, 4, false>),
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;
