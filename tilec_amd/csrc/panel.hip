@@ -7,29 +7,32 @@
 // space tilec/ext.py:29-51) and the 64x64 tile kernel's mostly empty tiles
 // (tilec/ext.py:13-24).  It is output-stationary: a workgroup owns one panel
 // of output columns — 512 bytes of each x2 row, 128 fp32 or 256 bf16
-// columns — and one K chunk; the grid is panels fastest, chunks slowest.
+// columns — and one K split; the grid is panels fastest, splits slowest.
 //
 // What sets the rate at the GEMV sizes (x2 of 64 MiB; MI355X, x2 rotated over
 // 512 MiB so every launch reads HBM), measured with per-workgroup
-// s_memrealtime timelines:
-//   * the workgroups in flight must read the same rows of x2 side by side:
-//     with panels fastest in the grid they cover whole 16 KiB rows at a time;
-//     chunk-major order (a panel's chunks consecutive) scatters the reads
-//     over many rows and loses ~25 %;
-//   * a workgroup's waves sweep down its chunk together: wave w takes row
+// s_memrealtime timelines and plain-read probes:
+//   * the workgroups in flight must read the same rows of x2 side by side.
+//     K is cut into batches of R = 64 rows and split s of S takes batches
+//     s, s + S, s + 2S, ...; with panels fastest in the grid the chip then
+//     reads one window of S batches of whole 16 KiB rows at a time.  A plain
+//     read of 64 MiB in that order took 10.6-11.0 us against 11.6 us with
+//     each workgroup reading one contiguous K chunk, and 12.5 us or more
+//     with pieces of 256 bytes or less per row;
+//   * a workgroup's waves sweep down each batch together: wave w takes row
 //     pairs w, w + W, ..., 32 lanes x 16 bytes per row;
 //   * about one workgroup of 8 waves per CU keeps the K split small, and
 //     the split's tail short: after its last row the workgroup adds its
 //     waves in LDS once, then wave 0 alone publishes the partial, counts
 //     itself in and, if last, adds the partials with every load issued at
 //     once.  That tail is three memory round trips (publish, count, read
-//     back) after the last row.
+//     back), about 1.8 us after the last row at K = N = 4096.
 //
 // Lane l: row rr = l / 32 of each row pair, 16-byte group cq = l % 32 of the
 // panel (CPL = 4 fp32 / 8 bf16 columns).  It accumulates out[m][col] for its
 // columns over its rows in plain FMAs (bf16 widened exactly, a 16-bit
 // shift), x1[m][row] coming from the cache.  Masking is on addresses: rows
-// past the chunk, columns past N and x1 rows past M load zeros without
+// past K, columns past N and x1 rows past M load zeros without
 // touching memory, from both operands.
 //
 // Split K: the workgroup publishes its partial with agent-coherent (sc1)
@@ -84,10 +87,13 @@ struct PanelGeom {
   int64_t panels, splits, kc;
 };
 
-// K chunk per split: a multiple of 16 rows, at most kc_max (the variant's
-// KC); the number of splits is raised to what kc_max needs and recomputed so
-// none is empty.
-PanelGeom panel_geom(int64_t N, int64_t K, int split_k, int pw, int kc_max) {
+// Splits of K.  A split takes the R-row batches (R = rows_per_batch, one
+// batch of the whole workgroup) split, split + S, split + 2S, ... of K, so
+// the workgroups in flight read one window of S neighbouring batches of x2
+// rows.  The split count is the request raised so that no split has more
+// than kc_max / R batches (the kernel's unrolled bound) and capped at the
+// number of batches (none is empty); kc = rows of the largest split.
+PanelGeom panel_geom(int64_t N, int64_t K, int split_k, int pw, int kc_max, int rows_per_batch) {
   PanelGeom g;
   g.panels = cdiv(N, pw);
   if (K <= 0) {
@@ -95,26 +101,28 @@ PanelGeom panel_geom(int64_t N, int64_t K, int split_k, int pw, int kc_max) {
     g.kc = 0;
     return g;
   }
+  const int64_t kblk = cdiv(K, rows_per_batch), per = kc_max / rows_per_batch;
   int64_t s = split_k < 1 ? 1 : split_k;
-  if (s < cdiv(K, kc_max)) s = cdiv(K, kc_max);
-  g.kc = cdiv(cdiv(K, s), 16) * 16;
-  g.splits = cdiv(K, g.kc);
+  s = std::max(s, cdiv(kblk, per));
+  s = std::min(s, kblk);
+  g.splits = s;
+  g.kc = cdiv(kblk, s) * rows_per_batch;
   return g;
 }
 
-template <typename T, int WAVES, int MV, bool CA, int KC>
+template <typename T, int WAVES, int MV, bool CA, int KC, int BT>
 __global__ __launch_bounds__(WAVES * 64) void panel_kernel(const T* __restrict__ x1, const T* __restrict__ x2,
                                                            float* __restrict__ out, int M, int N, int K,
-                                                           int64_t ldx1, int64_t ldx2, int64_t ldo, int kc,
+                                                           int64_t ldx1, int64_t ldx2, int64_t ldo,
                                                            unsigned* __restrict__ counters,
                                                            float* __restrict__ part) {
   static_assert(MV >= 1 && MV <= 4, "M <= 4");
-  static_assert(KC % (2 * WAVES * 8) == 0 && KC <= kKcMax, "whole batches of row pairs");
+  static_assert(KC % (2 * WAVES * BT) == 0 && KC <= kKcMax, "whole batches of row pairs");
   using E = PE<T>;
   typedef typename E::V V;
   constexpr int CPL = E::CPL, PW = kPanelOf<T>;
   constexpr int VPL = PW / 64;         // columns per lane of wave 0 after the reduction
-  constexpr int BT = 8;                // row pairs per batch
+  constexpr int R = 2 * WAVES * BT;    // rows of one workgroup batch
   constexpr int PPW = KC / (2 * WAVES);  // row pairs per wave at most
   constexpr uint32_t EB = E::BYTES;
   __shared__ float red[WAVES][MV][PW];
@@ -126,20 +134,20 @@ __global__ __launch_bounds__(WAVES * 64) void panel_kernel(const T* __restrict__
   const int panel = blockIdx.x, split = blockIdx.y;
   const int panels = gridDim.x, S = gridDim.y;
   const int n0 = panel * PW;
-  const int kbeg = split * kc;
-  const int nrows = max(0, min(K, kbeg + kc) - kbeg);  // kc <= KC
   const bool gok = n0 + CPL * cq < N;  // N % CPL == 0: the lane's group is all in or all out
+  // Batches of this split: global batches split, split + S, ... of R rows
+  // each (at most KC / R of them: the launcher's split count sees to it).
+  const int kblk = (K + R - 1) / R;
+  const int nbat = split < kblk ? (kblk - split + S - 1) / S : 0;
 
-  // One resource per operand, based at this chunk: 32-bit offsets (the
-  // launcher checks KC * ldx2 and KC * ldx1 fit).  Row pair p of the chunk
-  // (rows 2p, 2p + 1) belongs to wave p % W; pair j of this wave is
-  // p = j * W + wave.
-  const BufRsrc rx2 = make_rsrc(x2 + (int64_t)kbeg * ldx2 + n0);
-  const BufRsrc rx1 = make_rsrc(CA ? x1 + (int64_t)kbeg * ldx1 : x1 + kbeg);
+  // In a batch, row pair p (rows 2p, 2p + 1 of the batch) belongs to wave
+  // p % W; pair q of this wave is p = q * W + wave.  Resources are based at
+  // the batch: 32-bit offsets (the launcher checks KC * ldx2 and KC * ldx1
+  // fit, and R <= KC).
   auto x1_off = [&](int m, int row) -> uint32_t {
     return EB * (CA ? (uint32_t)row * (uint32_t)ldx1 + (uint32_t)m : (uint32_t)m * (uint32_t)ldx1 + (uint32_t)row);
   };
-  auto ld_x1 = [&](uint32_t o) -> float {
+  auto ld_x1 = [&](const BufRsrc& rx1, uint32_t o) -> float {
     if constexpr (sizeof(T) == 4) return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx1, (int)o, 0, 0));
     else return __int_as_float((int)__builtin_amdgcn_raw_buffer_load_b16(rx1, (int)o, 0, 0) << 16);
   };
@@ -149,28 +157,32 @@ __global__ __launch_bounds__(WAVES * 64) void panel_kernel(const T* __restrict__
   for (int m = 0; m < MV; ++m)
 #pragma unroll
     for (int c = 0; c < CPL; ++c) acc[m][c] = 0.f;
-  // Batches of BT row pairs, fully unrolled up to the chunk bound; a wave
-  // stops at its first batch past the chunk.  x1: every lane of a row needs
+  // Batches of BT row pairs per wave, fully unrolled up to KC / R; the
+  // workgroup stops after its last batch.  x1: every lane of a row needs
   // the same MV values; for M == 1 each lane loads its own (one address per
   // row), for M <= 4 lane cq < MV of the row loads x1[cq][row] and the row's
-  // lanes take them by shuffles.  Rows past the chunk load zeros from both
-  // operands.
+  // lanes take them by shuffles.  Rows past K load zeros from both operands.
 #pragma unroll
   for (int b0 = 0; b0 < PPW; b0 += BT) {
-    if (2 * (b0 * WAVES + wave) >= nrows) break;  // wave-uniform
+    const int bi = b0 / BT;
+    if (bi >= nbat) break;  // workgroup-uniform
+    const int kb = (bi * S + split) * R;
+    const BufRsrc rx2 = make_rsrc(x2 + (int64_t)kb * ldx2 + n0);
+    const BufRsrc rx1 = make_rsrc(CA ? x1 + (int64_t)kb * ldx1 : x1 + kb);
+    const int left = K - kb;  // rows of K from the batch's first row
     V v[BT];
     float a[BT][MV];
 #pragma unroll
     for (int q = 0; q < BT; ++q) {
-      const int row = 2 * ((b0 + q) * WAVES + wave) + rr;
-      const bool rok = row < nrows;
+      const int row = 2 * (q * WAVES + wave) + rr;
+      const bool rok = row < left;
       v[q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(
                                        rx2, (int)((rok & gok) ? EB * ((uint32_t)row * (uint32_t)ldx2 + (uint32_t)(CPL * cq)) : kOob),
                                        0, kCpolX2));
       if constexpr (MV == 1) {
-        a[q][0] = ld_x1((rok & (M > 0)) ? x1_off(0, row) : kOob);
+        a[q][0] = ld_x1(rx1, (rok & (M > 0)) ? x1_off(0, row) : kOob);
       } else {
-        const float mine = ld_x1((rok & (cq < MV) & (cq < M)) ? x1_off(cq, row) : kOob);
+        const float mine = ld_x1(rx1, (rok & (cq < MV) & (cq < M)) ? x1_off(cq, row) : kOob);
 #pragma unroll
         for (int m = 0; m < MV; ++m) a[q][m] = __shfl(mine, (lane & 32) + m);
       }
@@ -279,7 +291,7 @@ namespace {
 // Row-major x2 with 16-byte groups that never straddle N (N and ldx2
 // multiples of CPL, x2 16-byte aligned), M <= MV, x1 in either layout: the
 // panel kernel.  Anything else runs the streaming kernel with the same split.
-template <typename T, int WAVES, int MV, int KC>
+template <typename T, int WAVES, int MV, int KC, int BT>
 hipError_t launch_panel(const MatmulArgs& a) {
   constexpr int CPL = PE<T>::CPL, PW = kPanelOf<T>;
   constexpr int64_t EB = sizeof(T), lim = (int64_t(1) << 31) - 64;
@@ -288,18 +300,18 @@ hipError_t launch_panel(const MatmulArgs& a) {
   const bool fits = !(a.layout & TILEC_X2_COL_MAJOR) && a.M <= MV && a.N % CPL == 0 && a.ldx2 % CPL == 0 &&
                     aligned(a.x2, 16) && KC * a.ldx2 * EB < lim && (ca ? KC * a.ldx1 * EB : 4 * a.ldx1 * EB + KC * EB) < lim;
   if (!fits) return launch_skinny_fallback<T, 4, 2, MV>(a);
-  const PanelGeom g = panel_geom(a.N, a.K, a.split_k, PW, KC);
+  const PanelGeom g = panel_geom(a.N, a.K, a.split_k, PW, KC, 2 * WAVES * BT);
   unsigned* counters = g.splits > 1 ? a.counters : nullptr;
   float* part = g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr;
   const dim3 grid((unsigned)g.panels, (unsigned)g.splits);
   if (ca)
-    hipLaunchKernelGGL((panel_kernel<T, WAVES, MV, true, KC>), grid, dim3(WAVES * 64), 0, a.stream,
+    hipLaunchKernelGGL((panel_kernel<T, WAVES, MV, true, KC, BT>), grid, dim3(WAVES * 64), 0, a.stream,
                        static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K,
-                       a.ldx1, a.ldx2, a.ldo, (int)g.kc, counters, part);
+                       a.ldx1, a.ldx2, a.ldo, counters, part);
   else
-    hipLaunchKernelGGL((panel_kernel<T, WAVES, MV, false, KC>), grid, dim3(WAVES * 64), 0, a.stream,
+    hipLaunchKernelGGL((panel_kernel<T, WAVES, MV, false, KC, BT>), grid, dim3(WAVES * 64), 0, a.stream,
                        static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K,
-                       a.ldx1, a.ldx2, a.ldo, (int)g.kc, counters, part);
+                       a.ldx1, a.ldx2, a.ldo, counters, part);
   return hipGetLastError();
 }
 
@@ -311,26 +323,31 @@ hipError_t launch_panel(const MatmulArgs& a) {
 size_t skinny_counter_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 size_t skinny_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int split_k);
 
+// Rows of one workgroup batch of a panel variant (unroll = row pairs per
+// wave and batch).
+static int panel_batch_rows(const VariantDesc& d) { return 2 * d.waves * d.unroll; }
+
 size_t panel_workspace_bytes(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
-  const PanelGeom g = panel_geom(N, K, split_k, d.bn, d.bk);
+  const PanelGeom g = panel_geom(N, K, split_k, d.bn, d.bk, panel_batch_rows(d));
   const size_t own = g.splits > 1 ? (size_t)g.splits * g.panels * kRows * d.bn * sizeof(float) : 0;
   return std::max(own, skinny_workspace_bytes(d.dtype, M, N, K, split_k));
 }
 size_t panel_counter_bytes(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
-  const PanelGeom g = panel_geom(N, K, split_k, d.bn, d.bk);
+  const PanelGeom g = panel_geom(N, K, split_k, d.bn, d.bk, panel_batch_rows(d));
   const size_t own = g.splits > 1 ? (size_t)g.panels * kCounterStride * sizeof(unsigned) : 0;
   return std::max(own, skinny_counter_bytes(d.dtype, M, N, K, split_k));
 }
 
 // Variant table of this family (appended after the streaming and tile
 // tables, so earlier variant ids are unchanged).  BM = 16 rows (partial
-// slots), BN = panel width, BK = KC, the largest K chunk of one workgroup
-// (512 fp32 / 256 bf16 rows: one workgroup per CU at K = N = 4096),
-// max_m = MV; an automatic split aims at one workgroup per CU.
-static VariantDesc panel_desc(const char* name, int dtype, int waves, int max_m, int kc,
+// slots), BN = panel width, BK = KC, the most rows of K one workgroup takes
+// (512 fp32 / 256 bf16: one workgroup per CU at K = N = 4096), max_m = MV,
+// unroll = BT, row pairs per wave and batch (batches of 2 W BT = 64 rows);
+// an automatic split aims at one workgroup per CU.
+static VariantDesc panel_desc(const char* name, int dtype, int waves, int max_m, int kc, int bt,
                               hipError_t (*launch)(const MatmulArgs&)) {
   VariantDesc d{name, TILEC_FAMILY_SKINNY, dtype, kRows, dtype == TILEC_BF16 ? kPanelOf<u16> : kPanelOf<float>,
-                kc, waves, max_m, 2, launch};
+                kc, waves, max_m, bt, launch};
   d.workspace_bytes = panel_workspace_bytes;
   d.counter_bytes = panel_counter_bytes;
   d.wgs_per_cu = 1;
@@ -339,12 +356,12 @@ static VariantDesc panel_desc(const char* name, int dtype, int waves, int max_m,
 
 const VariantDesc* panel_variants(int* count) {
   static const VariantDesc t[] = {
-      panel_desc("skinny_f32_p_v1_w8", TILEC_F32, 8, 1, 512, launch_panel<float, 8, 1, 512>),
-      panel_desc("skinny_f32_p_v4_w8", TILEC_F32, 8, 4, 512, launch_panel<float, 8, 4, 512>),
-      panel_desc("skinny_bf16_p_v1_w8", TILEC_BF16, 8, 1, 256, launch_panel<u16, 8, 1, 256>),
-      panel_desc("skinny_bf16_p_v4_w8", TILEC_BF16, 8, 4, 256, launch_panel<u16, 8, 4, 256>),
-      panel_desc("skinny_f32_p_v1_w4", TILEC_F32, 4, 1, 512, launch_panel<float, 4, 1, 512>),
-      panel_desc("skinny_bf16_p_v1_w4", TILEC_BF16, 4, 1, 256, launch_panel<u16, 4, 1, 256>),
+      panel_desc("skinny_f32_p_v1_w8", TILEC_F32, 8, 1, 512, 4, launch_panel<float, 8, 1, 512, 4>),
+      panel_desc("skinny_f32_p_v4_w8", TILEC_F32, 8, 4, 512, 4, launch_panel<float, 8, 4, 512, 4>),
+      panel_desc("skinny_bf16_p_v1_w8", TILEC_BF16, 8, 1, 256, 4, launch_panel<u16, 8, 1, 256, 4>),
+      panel_desc("skinny_bf16_p_v4_w8", TILEC_BF16, 8, 4, 256, 4, launch_panel<u16, 8, 4, 256, 4>),
+      panel_desc("skinny_f32_p_v1_w4", TILEC_F32, 4, 1, 512, 8, launch_panel<float, 4, 1, 512, 8>),
+      panel_desc("skinny_bf16_p_v1_w4", TILEC_BF16, 4, 1, 256, 8, launch_panel<u16, 4, 1, 256, 8>),
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

@@ -15,15 +15,18 @@
 // once with 16-byte coalesced loads.
 //
 // Mapping.  A lane's 16-byte load of an x2 row holds CPL columns (4 fp32 or
-// 8 bf16); a workgroup owns a slab of 16*CPL output columns and one K chunk.
-// The chunk is walked in 16-row blocks; waves take interleaved blocks.  In a
+// 8 bf16); a workgroup owns a slab of 16*CPL output columns and one K split.
+// K is cut into 16-row blocks; with row-major x2, split s of S takes blocks
+// s, s + S, s + 2S, ... (the workgroups in flight then read neighbouring x2
+// rows), with column-major x2 a contiguous chunk of them; waves take
+// interleaved blocks of their workgroup's share.  In a
 // block, lane l (r = l / 16, q = l % 16) loads columns CPL*q .. of rows
 // 4r + u, u = 0..3 (four 16-byte loads; each wave load covers four 256-byte
 // row segments) and x1[q][4r .. 4r+3].  Row 4r + u is MFMA k-slot r of step
 // u of v_mfma_f32_16x16x4f32, and each of the CPL columns feeds one MFMA:
 //   D_c[m][q] += sum_r x1[m][4r+u] * x2[4r+u][SLAB*slab + CPL*q + c],
 // the A operand being exactly the lane's x1 value for (m = q, k-slot r).
-// Masking is done on addresses only: rows past the chunk, columns past N and
+// Masking is done on addresses only: rows past K, columns past N and
 // x1 rows past M get an out-of-range buffer offset and load zeros without
 // touching memory, so loaded registers go straight into the MFMAs.  Per
 // 4 KiB of x2 a wave issues 16 MFMAs for fp32 (512 cycles, 2.5x the rate the
@@ -149,6 +152,9 @@ struct SkinnyGeom {
 
 // K chunk per split: a multiple of kBlock rows, at most kKcMax; the number of
 // splits is raised to what kKcMax needs and recomputed so that none is empty.
+// Column-major x2 reads each split's chunk; row-major x2 only uses the split
+// count (its splits take interleaved blocks, kc rows each give or take one
+// block, and none is empty since splits <= cdiv(K, kBlock)).
 SkinnyGeom skinny_geom(int64_t M, int64_t N, int64_t K, int split_k, int slab) {
   SkinnyGeom g;
   g.nslabs = cdiv(N, slab);
@@ -211,23 +217,33 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
   const int n0 = slab * SLAB;
   const int col = n0 + CPL * q;
   const bool col_ok = col < N;
+  // Blocks of this split.  Row-major x2: split s takes the KB-row blocks s,
+  // s + S, s + 2S, ... of K, so the workgroups in flight read one window of
+  // S neighbouring blocks of x2 rather than S chunks far apart (a single
+  // 64 MiB read pass measured ~1 us faster in that order).  Column-major
+  // x2: the contiguous chunk kbeg .. kbeg + kc of every column.
   const int kbeg = split * kc;
   const int nrows = max(0, min(K, kbeg + kc) - kbeg);
-  const int nblocks = (nrows + KB - 1) / KB;
+  const int kblocks = (K + KB - 1) / KB;
+  const int nblocks = CB ? (nrows + KB - 1) / KB : (split < kblocks ? (kblocks - split + S - 1) / S : 0);
+  // First row of block b and the rows of K left from there (<= 0: past the
+  // end; such blocks load zeros).
+  auto blk_row = [&](int b) -> int { return CB ? kbeg + KB * b : KB * (b * S + split); };
+  auto blk_lim = [&](int b) -> int { return CB ? nrows - KB * b : K - KB * (b * S + split); };
 
-  // Block b covers rows kbeg + KB*b .. of K.  Resources are based at the
-  // block, so byte offsets stay small (the host bounds ldx1 and ldx2).
-  // Every mask is an out-of-range offset: the loaded registers feed the
-  // MFMAs directly, and a block past the chunk is all zeros (A and B).
+  // Resources are based at the block, so byte offsets stay small (the host
+  // bounds ldx1 and ldx2).  Every mask is an out-of-range offset: the loaded
+  // registers feed the MFMAs directly, and a block past the split's share is
+  // all zeros (A and B).
   const uint32_t col_off = EB * (uint32_t)col;
   const bool a_row = q < M;
-  // x1 element (row q, k = kbeg + brow + kr) of this lane: 0 if masked.
-  auto x1_off = [&](int brow, int kr) -> uint32_t {
-    if (!(a_row & (brow + kr < nrows))) return kOob;
+  // x1 element (row q, k = block row + kr) of this lane: 0 if masked.
+  auto x1_off = [&](int lim, int kr) -> uint32_t {
+    if (!(a_row & (kr < lim))) return kOob;
     return CA ? EB * ((uint32_t)kr * (uint32_t)ldx1 + (uint32_t)q) : EB * ((uint32_t)q * (uint32_t)ldx1 + (uint32_t)kr);
   };
-  auto x1_rsrc = [&](int brow) {
-    return make_rsrc(CA ? x1 + (int64_t)(kbeg + brow) * ldx1 : x1 + kbeg + brow);
+  auto x1_rsrc = [&](int k0) {
+    return make_rsrc(CA ? x1 + (int64_t)k0 * ldx1 : x1 + k0);
   };
   // Dword w of a 16-byte group from its elements' bit patterns h[].
   auto pack = [](const int* h, int w) -> int { return E::BYTES == 4 ? h[w] : (h[2 * w] | (h[2 * w + 1] << 16)); };
@@ -243,14 +259,14 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
     else return (int)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)o, 0, 0);
   };
   auto load_block = [&](int b, Block& blk) __attribute__((always_inline)) {
-    const int brow = KB * b;  // wave-uniform, relative to kbeg
-    const BufRsrc rx1 = x1_rsrc(brow);
+    const int k0 = blk_row(b), lim = blk_lim(b);  // wave-uniform
+    const BufRsrc rx1 = x1_rsrc(k0);
     if constexpr (!CB) {
-      const BufRsrc rx2 = make_rsrc(x2 + (int64_t)(kbeg + brow) * ldx2);
+      const BufRsrc rx2 = make_rsrc(x2 + (int64_t)k0 * ldx2);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int row = 4 * r + u;
-        const bool ok = brow + row < nrows;
+        const bool ok = row < lim;
         const uint32_t roff = EB * (uint32_t)row * (uint32_t)ldx2;
         if constexpr (VEC) {
           const uint32_t o = (ok & col_ok) ? roff + col_off : kOob;
@@ -264,11 +280,11 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
         }
       }
       if constexpr (MV > 0) {
-        // x1[m][4r .. 4r+3] for every row m < MV: 0 past M or past the chunk
+        // x1[m][4r .. 4r+3] for every row m < MV: 0 past M or past K
 #pragma unroll
         for (int m = 0; m < (MV > 0 ? MV : 1); ++m) {
           auto off = [&](int kr) -> uint32_t {
-            if (!((m < M) & (brow + kr < nrows))) return kOob;
+            if (!((m < M) & (kr < lim))) return kOob;
             return CA ? EB * ((uint32_t)kr * (uint32_t)ldx1 + (uint32_t)m) : EB * ((uint32_t)m * (uint32_t)ldx1 + (uint32_t)kr);
           };
           if constexpr (VEC && !CA) {
@@ -286,14 +302,14 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
             }
           }
         }
-      } else if constexpr (VEC && !CA) {  // x1[q][4r .. 4r+3]; K % 4 == 0: the 4 k of a lane are all valid or all past the chunk
-        const uint32_t o = x1_off(brow, 4 * r);
+      } else if constexpr (VEC && !CA) {  // x1[q][4r .. 4r+3]; K % 4 == 0: the 4 k of a lane are all valid or all past K
+        const uint32_t o = x1_off(lim, 4 * r);
         if constexpr (CPL == 4) blk.a = load_f32x4(rx1, o);
         else blk.a = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(rx1, (int)o, 0, 0));
       } else {
         int h[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) h[u] = ld_elem(rx1, x1_off(brow, 4 * r + u));
+        for (int u = 0; u < 4; ++u) h[u] = ld_elem(rx1, x1_off(lim, 4 * r + u));
         if constexpr (CPL == 4) {
           put(blk.a, h);
         } else {
@@ -302,8 +318,8 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
         }
       }
     } else {
-      // x2 column-major: columns n0 + 16g + q, k = kbeg + brow + EPL*r ..
-      const BufRsrc rx2 = make_rsrc(x2 + (int64_t)n0 * ldx2 + kbeg + brow);
+      // x2 column-major: columns n0 + 16g + q, k = k0 + EPL*r ..
+      const BufRsrc rx2 = make_rsrc(x2 + (int64_t)n0 * ldx2 + k0);
       const int kr = EPL * r;
 #pragma unroll
       for (int g = 0; g < CPL; ++g) {
@@ -311,22 +327,22 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
         const bool nok = n0 + n < N;
         const uint32_t noff = EB * ((uint32_t)n * (uint32_t)ldx2 + (uint32_t)kr);
         if constexpr (VEC) {  // K % EPL == 0: a lane's EPL k are all valid or all past the chunk
-          const uint32_t o = (nok & (brow + kr < nrows)) ? noff : kOob;
+          const uint32_t o = (nok & (kr < lim)) ? noff : kOob;
           blk.b[g] = __builtin_bit_cast(decltype(blk.a), __builtin_amdgcn_raw_buffer_load_b128(rx2, (int)o, 0, kCpolX2));
         } else {
           int h[EPL];
 #pragma unroll
-          for (int e = 0; e < EPL; ++e) h[e] = ld_elem(rx2, (nok & (brow + kr + e < nrows)) ? noff + EB * e : kOob);
+          for (int e = 0; e < EPL; ++e) h[e] = ld_elem(rx2, (nok & (kr + e < lim)) ? noff + EB * e : kOob);
           put(blk.b[g], h);
         }
       }
       // x1[q][kr .. kr + EPL-1]
       if constexpr (VEC && !CA) {
-        blk.a = __builtin_bit_cast(decltype(blk.a), __builtin_amdgcn_raw_buffer_load_b128(rx1, (int)x1_off(brow, kr), 0, 0));
+        blk.a = __builtin_bit_cast(decltype(blk.a), __builtin_amdgcn_raw_buffer_load_b128(rx1, (int)x1_off(lim, kr), 0, 0));
       } else {
         int h[EPL];
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) h[e] = ld_elem(rx1, x1_off(brow, kr + e));
+        for (int e = 0; e < EPL; ++e) h[e] = ld_elem(rx1, x1_off(lim, kr + e));
         put(blk.a, h);
       }
     }
@@ -396,7 +412,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
   // Two register sets used in turn: the next batch's loads are in flight
   // while the current batch's MFMAs run.  The body is one basic block and
   // sched_barrier keeps "issue the next batch, then the MFMAs of the current
-  // one".  Loads past the chunk return zeros without memory traffic.
+  // one".  Loads past the split's share return zeros without memory traffic.
   Block A[UB], B[UB];
   if (nb > 0) {
 #pragma unroll
