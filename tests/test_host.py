@@ -79,6 +79,11 @@ def test_cpu_tensors_raise_not_fallback():
 
 def test_hip_configs_rules():
     names = {v["name"]: v for v in _lib.variants()}
+    # the direct family past the small-output rule: up to four 64x64 tiles per CU, fp32 only
+    assert ext.direct_regime(1024, 1024, "f32") and ext.direct_regime(2048, 2048, "f32")
+    assert not ext.direct_regime(2049, 2048, "f32") and not ext.direct_regime(1024, 1024, "bf16")
+    assert any(c[0].startswith("direct_") for c in ext.hip_configs(1024, 1024, 1024, "f32"))
+    assert not any(c[0].startswith("direct_") for c in ext.hip_configs(4096, 4096, 4096, "f32"))
     for M, K, N, dt in [(1, 4096, 4096, "f32"), (16, 4096, 4096, "f32"), (17, 4096, 4096, "f32"),
                         (4096, 4096, 4096, "f32"), (8192, 8192, 8192, "bf16"), (3, 100, 7, "f32"),
                         (1, 4096, 4096, "bf16"), (1024, 1024, 1024, "f32"), (520, 8192, 1648, "bf16")]:
@@ -93,7 +98,8 @@ def test_hip_configs_rules():
                 assert eff == 1 or K // eff >= 16 * v["waves"]
             elif v["family"] == _lib.FAMILY_DIRECT:
                 eff = ext._direct_splits(K, s)
-                assert dt == "f32" and ext.skinny_regime(M, N, dt) and v["bm"] < 2 * max(M, 16)
+                assert dt == "f32" and v["bm"] < 2 * max(M, 16)
+                assert ext.skinny_regime(M, N, dt) or ext.direct_regime(M, N, dt)
                 assert eff == 1 or ext.cdiv(K, eff) >= 16 * v["waves"]
             else:
                 tiles = ext.cdiv(M, v["bm"]) * ext.cdiv(N, v["bn"])

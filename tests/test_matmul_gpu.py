@@ -308,16 +308,18 @@ def direct_variants():
 
 
 DIRECT_SHAPES = [(1, 4096, 4096), (4, 4096, 4096), (16, 4096, 4096), (7, 1000, 65), (16, 37, 3001),
-                 (513, 3001, 127), (127, 1000, 513), (512, 4096, 64), (100, 4097, 33), (33, 16, 1)]
+                 (513, 3001, 127), (127, 1000, 513), (512, 4096, 64), (100, 4097, 33), (33, 16, 1),
+                 (1024, 1024, 1024), (1100, 333, 1500)]
 
 
 def test_direct_kernel():
     """The direct-operand MFMA kernel (operands loaded straight into MFMA
-    registers, K split over waves and workgroups): the GEMV and small-output
-    BASELINE shapes plus ragged ones (K and N not multiples of 4, M past a
-    tile), every layout, unsplit and split K, against the fp64 oracle."""
+    registers, K split over waves and workgroups): the GEMV, small-output and
+    1024^3 BASELINE shapes plus ragged ones (K and N not multiples of 4, M
+    past a tile), every layout, unsplit and split K, against the fp64
+    oracle."""
     dv = direct_variants()
-    assert len(dv) == 7
+    assert len(dv) == 11
     for i, (m, k, n) in enumerate(DIRECT_SHAPES):
         a, b = O.normal((m, k), 1100 + 2 * i), O.normal((k, n), 1101 + 2 * i)
         ref = O.matmul_f64(a, b)

@@ -81,8 +81,9 @@ struct Frag {
 
 // CA: x1 column-major (x1[m + k * ldx1]); CB: x2 column-major (x2[k + n *
 // ldx2]); NT2: x2 is streamed once (non-temporal loads); BT: steps per
-// batch of loads.
-template <int TI, int TJ, int W, int BT, bool CA, bool CB, bool NT2>
+// batch of loads; PIPE: two register sets, the next batch's loads issued
+// before the current batch's MFMAs.
+template <int TI, int TJ, int W, int BT, bool CA, bool CB, bool NT2, bool PIPE>
 __global__ __launch_bounds__(W * 64) void direct_kernel(const float* __restrict__ x1, const float* __restrict__ x2,
                                                         float* __restrict__ out, int M, int N, int K, int64_t ldx1,
                                                         int64_t ldx2, int64_t ldo, int kc, int tiles_n,
@@ -186,13 +187,32 @@ __global__ __launch_bounds__(W * 64) void direct_kernel(const float* __restrict_
     }
   };
 
-  for (int b = 0; b < nb; ++b) {
-    Frag<TI, TJ, BT> f;
-    load(f, b);
-    // Keep every load of the batch ahead of the first MFMA (the scheduler
-    // would otherwise interleave them to save registers, and wait for each).
-    __builtin_amdgcn_sched_barrier(0);
-    compute(f, b);
+  if constexpr (PIPE) {
+    // Batch b + 1 is in flight while batch b is multiplied; a load past the
+    // wave's last batch is masked (valid <= 0) and touches no memory.
+    Frag<TI, TJ, BT> fa, fb;
+    if (nb > 0) load(fa, 0);
+    int b = 0;
+    for (; b + 1 < nb; b += 2) {
+      load(fb, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(fa, b);
+      __builtin_amdgcn_sched_barrier(0);
+      load(fa, b + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(fb, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (b < nb) compute(fa, b);
+  } else {
+    for (int b = 0; b < nb; ++b) {
+      Frag<TI, TJ, BT> f;
+      load(f, b);
+      // Keep every load of the batch ahead of the first MFMA (the scheduler
+      // would otherwise interleave them to save registers, and wait for each).
+      __builtin_amdgcn_sched_barrier(0);
+      compute(f, b);
+    }
   }
 
   // The waves meet in LDS; thread (w, l) then owns results w, w + W, ... of
@@ -276,9 +296,9 @@ constexpr size_t direct_lds_bytes() {
   return (size_t)W * 4 * TI * TJ * 64 * sizeof(f32x4) + 16;
 }
 
-template <int TI, int TJ, int W, int BT, bool NT2, bool CA, bool CB>
+template <int TI, int TJ, int W, int BT, bool NT2, bool PIPE, bool CA, bool CB>
 hipError_t launch_direct_layout(const MatmulArgs& a, const DirectGeom& g) {
-  auto k = direct_kernel<TI, TJ, W, BT, CA, CB, NT2>;
+  auto k = direct_kernel<TI, TJ, W, BT, CA, CB, NT2, PIPE>;
   constexpr size_t lds = direct_lds_bytes<TI, TJ, W>();
   static std::atomic<uint64_t> lds_devices{0};
   const hipError_t e = raise_lds_limit((const void*)k, lds, lds_devices);
@@ -290,7 +310,7 @@ hipError_t launch_direct_layout(const MatmulArgs& a, const DirectGeom& g) {
   return hipGetLastError();
 }
 
-template <int TI, int TJ, int W, int BT, bool NT2>
+template <int TI, int TJ, int W, int BT, bool NT2, bool PIPE = false>
 hipError_t launch_direct(const MatmulArgs& a) {
   const DirectGeom g = direct_geom(a.M, a.N, a.K, a.split_k, 16 * TI, 64 * TJ);
   if (g.tiles_m * g.tiles_n == 0) return hipSuccess;
@@ -298,10 +318,10 @@ hipError_t launch_direct(const MatmulArgs& a) {
   // tile GEMM, which addresses such operands itself and needs no scratch.
   if (!direct_offsets_fit(a, g, 16 * TI, 64 * TJ)) return launch_gemm_f32_unsplit(a);
   switch (a.layout & 3) {
-    case 0: return launch_direct_layout<TI, TJ, W, BT, NT2, false, false>(a, g);
-    case TILEC_X1_COL_MAJOR: return launch_direct_layout<TI, TJ, W, BT, NT2, true, false>(a, g);
-    case TILEC_X2_COL_MAJOR: return launch_direct_layout<TI, TJ, W, BT, NT2, false, true>(a, g);
-    default: return launch_direct_layout<TI, TJ, W, BT, NT2, true, true>(a, g);
+    case 0: return launch_direct_layout<TI, TJ, W, BT, NT2, PIPE, false, false>(a, g);
+    case TILEC_X1_COL_MAJOR: return launch_direct_layout<TI, TJ, W, BT, NT2, PIPE, true, false>(a, g);
+    case TILEC_X2_COL_MAJOR: return launch_direct_layout<TI, TJ, W, BT, NT2, PIPE, false, true>(a, g);
+    default: return launch_direct_layout<TI, TJ, W, BT, NT2, PIPE, true, true>(a, g);
   }
 }
 
@@ -320,9 +340,9 @@ size_t direct_counter_bytes(const VariantDesc& d, int64_t M, int64_t N, int64_t 
   return (size_t)(g.tiles_m * g.tiles_n * kSplitCounterStride * sizeof(unsigned));
 }
 
-VariantDesc direct_desc(const char* name, int ti, int tj, int waves, int bt,
+VariantDesc direct_desc(const char* name, int ti, int tj, int waves, int bt, bool pipe,
                         hipError_t (*launch)(const MatmulArgs&)) {
-  VariantDesc d{name, TILEC_FAMILY_DIRECT, TILEC_F32, 16 * ti, 64 * tj, kStep, waves, 0, bt, launch};
+  VariantDesc d{name, TILEC_FAMILY_DIRECT, TILEC_F32, 16 * ti, 64 * tj, kStep, waves, 0, pipe ? 2 * bt : bt, launch};
   d.workspace_bytes = direct_workspace_bytes;
   d.counter_bytes = direct_counter_bytes;
   d.wgs_per_cu = waves >= 8 ? 1 : 2;
@@ -336,20 +356,28 @@ int64_t direct_effective_splits(int64_t K, int split_k) { return direct_geom(1, 
 
 // Variant table of this family (appended after the earlier tables, so their
 // variant ids are unchanged).  BM x BN = the output tile, BK = the 16-row
-// step, unroll = steps per batch of loads.  The 16 x 128 tile with 8 waves
-// streams x2 once (non-temporal loads, one workgroup per CU); the others are
-// for small-output GEMMs.
+// step, unroll = steps of loads a wave has in flight (BT, or 2 BT with two
+// register sets).  The 16 x 128 tile with 8 waves streams x2 once
+// (non-temporal loads, one workgroup per CU); the others are for
+// small-output GEMMs.
 const VariantDesc* direct_variants(int* count) {
   static const VariantDesc t[] = {
-      direct_desc("direct_f32_16x128_w8", 1, 2, 8, 4, launch_direct<1, 2, 8, 4, true>),
-      direct_desc("direct_f32_16x64_w4", 1, 1, 4, 8, launch_direct<1, 1, 4, 8, false>),
-      direct_desc("direct_f32_32x64_w4", 2, 1, 4, 6, launch_direct<2, 1, 4, 6, false>),
-      direct_desc("direct_f32_32x128_w4", 2, 2, 4, 4, launch_direct<2, 2, 4, 4, false>),
-      direct_desc("direct_f32_64x64_w4", 4, 1, 4, 4, launch_direct<4, 1, 4, 4, false>),
+      direct_desc("direct_f32_16x128_w8", 1, 2, 8, 4, false, launch_direct<1, 2, 8, 4, true>),
+      direct_desc("direct_f32_16x64_w4", 1, 1, 4, 8, false, launch_direct<1, 1, 4, 8, false>),
+      direct_desc("direct_f32_32x64_w4", 2, 1, 4, 6, false, launch_direct<2, 1, 4, 6, false>),
+      direct_desc("direct_f32_32x128_w4", 2, 2, 4, 4, false, launch_direct<2, 2, 4, 4, false>),
+      direct_desc("direct_f32_64x64_w4", 4, 1, 4, 4, false, launch_direct<4, 1, 4, 4, false>),
       // 8 waves (two per SIMD) on the small tiles: one wave's loads wait
       // while the other's MFMAs run
-      direct_desc("direct_f32_16x64_w8", 1, 1, 8, 4, launch_direct<1, 1, 8, 4, false>),
-      direct_desc("direct_f32_32x64_w8", 2, 1, 8, 4, launch_direct<2, 1, 8, 4, false>),
+      direct_desc("direct_f32_16x64_w8", 1, 1, 8, 4, false, launch_direct<1, 1, 8, 4, false>),
+      direct_desc("direct_f32_32x64_w8", 2, 1, 8, 4, false, launch_direct<2, 1, 8, 4, false>),
+      // Two register sets: a wave's next batch loads while its current one
+      // is multiplied, so K chunks of several batches (fewer splits, a
+      // shorter combine) do not pay the memory latency per batch
+      direct_desc("direct_f32_16x64_w8_db", 1, 1, 8, 4, true, launch_direct<1, 1, 8, 4, false, true>),
+      direct_desc("direct_f32_16x64_w4_db", 1, 1, 4, 3, true, launch_direct<1, 1, 4, 3, false, true>),
+      direct_desc("direct_f32_32x64_w4_db", 2, 1, 4, 2, true, launch_direct<2, 1, 4, 2, false, true>),
+      direct_desc("direct_f32_32x64_w8_db", 2, 1, 8, 3, true, launch_direct<2, 1, 8, 3, false, true>),
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

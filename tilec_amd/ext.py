@@ -86,7 +86,8 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
     The skinny family (a K split, 16-row blocks) and the direct family (fp32
     MFMAs on operands loaded straight into registers, a K split) are offered
     for M <= 16 and, for fp32, outputs too small to fill the chip with 64x64
-    tiles; the tile GEMMs
+    tiles; the direct family also for fp32 outputs of up to four such tiles
+    per CU (direct_regime); the tile GEMMs
     take any M, and K splits too when their own tiles cannot fill the CUs
     (for tiles small enough to split, at least 4 K steps per split).  This
     is the search space of tune.bench / tune.pick, as `mm_configs` is for
@@ -108,7 +109,7 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
         elif v["family"] == _lib.FAMILY_DIRECT:
             # Any split that leaves every wave at least one 16-row step;
             # no tile more than twice as tall as M needs.
-            if not skinny_regime(M, N, code) or v["bm"] >= 2 * max(M, 16):
+            if not (skinny_regime(M, N, code) or direct_regime(M, N, code)) or v["bm"] >= 2 * max(M, 16):
                 continue
             # Splits that fill the CUs exactly once or twice over are
             # offered beside the powers of two.
@@ -199,6 +200,15 @@ def skinny_regime(M, N, dtype="f32"):
     if M <= 16:
         return True
     return _dtype_code_name(dtype) == _lib.F32 and cdiv(M, 64) * cdiv(N, 64) < SMALL_OUTPUT_TILES
+
+
+def direct_regime(M, N, dtype="f32"):
+    """Whether the direct-operand kernel is also a candidate past the
+    small-output rule: fp32 outputs of up to four 64x64 tiles per CU
+    (1024^2 .. 2048^2-sized), where the tile GEMMs' large tiles leave CUs
+    idle or need a K split and the direct kernel's 32x64 tiles (two register
+    sets of operands in flight) fill the chip unsplit."""
+    return _dtype_code_name(dtype) == _lib.F32 and cdiv(M, 64) * cdiv(N, 64) <= 4 * SMALL_OUTPUT_TILES
 
 
 def _skinny_splits(K, split_k, kc_max):
