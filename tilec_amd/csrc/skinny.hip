@@ -16,9 +16,9 @@
 //
 // Mapping.  A lane's 16-byte load of an x2 row holds CPL columns (4 fp32 or
 // 8 bf16); a workgroup owns a slab of 16*CPL output columns and one K split.
-// K is cut into 16-row blocks; with row-major x2, split s of S takes blocks
-// s, s + S, s + 2S, ... (the workgroups in flight then read neighbouring x2
-// rows), with column-major x2 a contiguous chunk of them; waves take
+// K is cut into 16-row blocks; with row-major x2 and M <= 16, split s of S
+// takes blocks s, s + S, s + 2S, ... (the workgroups in flight then read
+// neighbouring x2 rows), otherwise a contiguous chunk of them; waves take
 // interleaved blocks of their workgroup's share.  In a
 // block, lane l (r = l / 16, q = l % 16) loads columns CPL*q .. of rows
 // 4r + u, u = 0..3 (four 16-byte loads; each wave load covers four 256-byte
@@ -152,7 +152,8 @@ struct SkinnyGeom {
 
 // K chunk per split: a multiple of kBlock rows, at most kKcMax; the number of
 // splits is raised to what kKcMax needs and recomputed so that none is empty.
-// Column-major x2 reads each split's chunk; row-major x2 only uses the split
+// Column-major x2, and row-major x2 with more than one 16-row block of x1,
+// read each split's chunk; row-major x2 with M <= 16 only uses the split
 // count (its splits take interleaved blocks, kc rows each give or take one
 // block, and none is empty since splits <= cdiv(K, kBlock)).
 SkinnyGeom skinny_geom(int64_t M, int64_t N, int64_t K, int split_k, int slab) {
@@ -217,19 +218,22 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
   const int n0 = slab * SLAB;
   const int col = n0 + CPL * q;
   const bool col_ok = col < N;
-  // Blocks of this split.  Row-major x2: split s takes the KB-row blocks s,
-  // s + S, s + 2S, ... of K, so the workgroups in flight read one window of
-  // S neighbouring blocks of x2 rather than S chunks far apart (a single
-  // 64 MiB read pass measured ~1 us faster in that order).  Column-major
-  // x2: the contiguous chunk kbeg .. kbeg + kc of every column.
+  // Blocks of this split.  Row-major x2 with one row block (M <= 16): split
+  // s takes the KB-row blocks s, s + S, s + 2S, ... of K, so the workgroups
+  // in flight read one window of S neighbouring blocks of x2 rather than S
+  // chunks far apart (a single 64 MiB read pass measured ~1 us faster in
+  // that order).  Otherwise the contiguous chunk kbeg .. kbeg + kc: with
+  // more row blocks x1 is large, and interleaved 16-row blocks would cut its
+  // rows into 64-byte pieces whose 128-byte lines two splits both fetch.
+  const bool inter = !CB && gridDim.z == 1;  // workgroup-uniform
   const int kbeg = split * kc;
   const int nrows = max(0, min(K, kbeg + kc) - kbeg);
   const int kblocks = (K + KB - 1) / KB;
-  const int nblocks = CB ? (nrows + KB - 1) / KB : (split < kblocks ? (kblocks - split + S - 1) / S : 0);
+  const int nblocks = inter ? (split < kblocks ? (kblocks - split + S - 1) / S : 0) : (nrows + KB - 1) / KB;
   // First row of block b and the rows of K left from there (<= 0: past the
   // end; such blocks load zeros).
-  auto blk_row = [&](int b) -> int { return CB ? kbeg + KB * b : KB * (b * S + split); };
-  auto blk_lim = [&](int b) -> int { return CB ? nrows - KB * b : K - KB * (b * S + split); };
+  auto blk_row = [&](int b) -> int { return inter ? KB * (b * S + split) : kbeg + KB * b; };
+  auto blk_lim = [&](int b) -> int { return inter ? K - KB * (b * S + split) : nrows - KB * b; };
 
   // Resources are based at the block, so byte offsets stay small (the host
   // bounds ldx1 and ldx2).  Every mask is an out-of-range offset: the loaded
