@@ -22,7 +22,8 @@ and W warmup steps.  Extra objects in the same line:
                  W [N, K] row-major) as in `skinny`, and the 4096^3 fp32 /
                  8192^3 bf16 GEMMs with x1, x2 or both column-major
   reduce       — row and column sums (ext.sum, the reference's tl.sum) in
-                 HBM GB/s, graph-replayed over rotating inputs
+                 HBM GB/s, graph-replayed over rotating inputs, beside
+                 torch.sum of the same inputs timed the same way
   vendor_torch_mm — the square fp32, config-4 bf16 and GEMV cases through
                  torch.mm (hipBLASLt / rocBLAS, fp32 result) on the same
                  box, data and timing protocol, for reference
@@ -363,7 +364,9 @@ REDUCE_CASES = (
 
 def bench_reduce(reps=8):
     """Row and column sums (ext.sum): HBM GB/s from graph-replayed calls over
-    rotating inputs (>= 512 MB in total, beyond the Infinity Cache)."""
+    rotating inputs (>= 512 MB in total, beyond the Infinity Cache), and the
+    vendor's own sum of the same inputs (torch.sum over the same axis, fp32
+    accumulate and out) timed the same way."""
     import torch
     from oracle import oracle as O
     from tilec_amd import ext
@@ -375,26 +378,35 @@ def bench_reduce(reps=8):
         esz = 4 if dtype == "f32" else 2
         nbuf = max(2, (512 << 20) // (esz * R * C))
         xs = [torch.from_numpy(O.normal((R, C), 2000 + 10 * i + j)).to(tdt).cuda() for j in range(nbuf)]
-        for x in xs:  # workspace exists before capture
-            ext.sum(x, axis)
-        torch.cuda.synchronize()
         calls = 4 * nbuf
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            ext.sum(xs[0], axis)
+
+        def per_call_ms(fn):
+            for x in xs:  # workspace exists before capture
+                fn(x)
             torch.cuda.synchronize()
-            with torch.cuda.graph(g, stream=s):
-                outs = [ext.sum(xs[j % nbuf], axis) for j in range(calls)]
-        torch.cuda.synchronize()
-        with torch.cuda.stream(s):
-            ms = timed(g.replay, reps, 2, stream=s) / calls
-        del outs, xs
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                fn(xs[0])
+                torch.cuda.synchronize()
+                with torch.cuda.graph(g, stream=s):
+                    outs = [fn(xs[j % nbuf]) for j in range(calls)]
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                ms = timed(g.replay, reps, 2, stream=s) / calls
+            del outs, g
+            return ms
+
+        ms = per_call_ms(lambda x: ext.sum(x, axis))
+        vms = per_call_ms(lambda x: torch.sum(x, dim=axis, dtype=torch.float32))
+        del xs
         nbytes = esz * R * C + 4 * (R if axis == 1 else C)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        out[name] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, traffic=traffic_of("sum", R, C, axis))
-        log(f"sum {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM:.1f}% of HBM)")
+        out[name] = dict(us=ms * 1e3, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, traffic=traffic_of("sum", R, C, axis),
+                         torch_sum_us=vms * 1e3, torch_sum_frac=nbytes / (vms * 1e-3) / 1e9 / PEAK_HBM)
+        log(f"sum {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM:.1f}% of HBM); "
+            f"torch.sum {vms * 1e3:.2f} us")
     return out
 
 
