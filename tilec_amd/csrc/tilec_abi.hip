@@ -171,6 +171,13 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
     // across workgroups (on MI355X within 1.15x of the best measured config
     // for such shapes, geometric mean; the streaming kernel: 1.9x).
     if (small_output(M, N)) return find("direct_f32_32x64_w4");
+    // Up to four 64x64 tiles per CU but too few 128x128 tiles to give each CU
+    // one (1024^2-sized outputs): the direct kernel's 32x64 tile with two
+    // register sets, unsplit or nearly (on MI355X within 1.10x of the best
+    // measured config over the 53 such and larger fp32 shapes timed,
+    // geometric mean; the tile GEMMs below alone: 1.37x).
+    if (cdiv(M, 128) * cdiv(N, 128) < cus && cdiv(M, 64) * cdiv(N, 64) <= 4 * (int64_t)cus)
+      return find("direct_f32_32x64_w4_db");
     static const char* order[] = {"gemm_f32_256x256x32_w2x4", "gemm_f32_256x128x16_w2x2",
                                   "gemm_f32_128x128x32_w2x4", "gemm_f32_128x64x16_w2x2"};
     for (const char* nm : order) {
