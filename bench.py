@@ -27,6 +27,9 @@ and W warmup steps.  Extra objects in the same line:
   vendor_torch_mm — the square fp32, config-4 bf16 and GEMV cases through
                  torch.mm (hipBLASLt / rocBLAS, fp32 result) on the same
                  box, data and timing protocol, for reference
+  tuner_unseen — the tuner's model on shapes absent from its timing table:
+                 its pick against the best of every offered config, timed
+                 with the tuner's own protocol, beside its held-out report
   host_overhead — eager wall time per ext.matrix_mul call (Python, ctypes,
                  launch) for a 1x1x1 product, a ragged small-output shape and
                  the M=1 GEMV, next to their device time per call
@@ -40,6 +43,7 @@ Only one GPU: --gpus above 1 exits with a message.
 
 import argparse
 import json
+import math
 import os
 import platform
 import sys
@@ -65,7 +69,7 @@ def parse():
                    help="with --only skinny, configs or reduce: run only the cases whose key contains this "
                         "text (one kernel per profile run)")
     p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "vendor", "copy",
-                                      "host", "cpu"],
+                                      "host", "tuner", "cpu"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -410,6 +414,51 @@ def bench_reduce(reps=8):
     return out
 
 
+# Shapes absent from the tuner's timing table (tilec_amd/mm_bench_mi355x.csv),
+# one or more per regime: GEMV, small output, medium, large fp32 and bf16.
+TUNER_UNSEEN = [(5, 3000, 2500, "f32"), (12, 6000, 1000, "bf16"), (48, 2900, 1800, "f32"), (96, 4000, 640, "f32"),
+                (200, 1500, 3000, "f32"), (777, 777, 777, "f32"), (1500, 3100, 900, "f32"),
+                (2000, 3000, 1000, "bf16"), (3000, 2000, 5000, "bf16")]
+
+
+def bench_tuner():
+    """The tuner on shapes it has never timed, where `tune.pick` answers from
+    its model rather than its measured-best table: the pick against the best
+    of every config `hip_configs` offers, all timed with the tuner's own
+    protocol (`tune.time_ms`, x2 rotated as in its table), beside the
+    held-out report stored with the model."""
+    import torch
+    from tilec_amd import tune, ext
+    model = tune._model()
+    g = torch.Generator(device="cuda").manual_seed(0)
+    cases = []
+    for M, K, N, dtype in TUNER_UNSEEN:
+        if CASE is not None and CASE not in f"{M}x{K}x{N}_{dtype}":
+            continue
+        assert (M, K, N, dtype, 0) not in model.best, "an unseen shape is in the tuner's table"
+        pick = tuple(tune.pick(M, K, N, dtype, 0))
+        x1, x2 = tune.operands(M, K, N, dtype, 0, g)
+        x2s = tune.operands_for(M, K, N, x2)
+        tune.settle(x1, x2, pick)
+        t_pick = tune.time_ms(x1, x2, pick, None, x2s=x2s)
+        best_t, best_c = t_pick, pick
+        for c in ext.hip_configs(M, K, N, dtype, 0):
+            if tuple(c) == pick:
+                continue
+            t = tune.time_ms(x1, x2, c, best_t, x2s=x2s)
+            if t < best_t:
+                best_t, best_c = t, tuple(c)
+        del x1, x2, x2s
+        cases.append(dict(shape=[M, K, N], dtype=dtype, pick=list(pick), pick_us=t_pick * 1e3, best=list(best_c),
+                          best_us=best_t * 1e3, ratio=t_pick / best_t))
+        log(f"tuner {M}x{K}x{N} {dtype}: pick {pick} {t_pick * 1e3:.1f} us, best {best_c} {best_t * 1e3:.1f} us "
+            f"({t_pick / best_t:.2f}x)")
+    ratios = [c["ratio"] for c in cases]
+    geo = math.exp(sum(math.log(r) for r in ratios) / len(ratios)) if ratios else None
+    return dict(unseen_shapes=len(cases), geomean_vs_best=geo, worst_vs_best=max(ratios) if ratios else None,
+                cases=cases, held_out_report=getattr(model, "report", None))
+
+
 def bench_copy(nbytes=256 << 20, reps=10):
     """A plain device-to-device copy of known size: what FETCH_SIZE and
     WRITE_SIZE read for it calibrates those counters."""
@@ -590,7 +639,7 @@ def main():
     if args.only:
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
                "configs": bench_configs, "layouts": bench_layouts, "reduce": bench_reduce,
-               "vendor": bench_vendor, "copy": bench_copy, "host": bench_host,
+               "vendor": bench_vendor, "copy": bench_copy, "host": bench_host, "tuner": bench_tuner,
                "cpu": lambda: bench_cpu(args.cpu_seconds)}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return
@@ -604,6 +653,7 @@ def main():
         extra["layouts"] = bench_layouts()
         extra["reduce"] = bench_reduce()
         extra["host_overhead"] = bench_host()
+        extra["tuner_unseen"] = bench_tuner()
         extra["vendor_torch_mm"] = bench_vendor()
     cpu = None if args.no_cpu else bench_cpu(args.cpu_seconds)
 

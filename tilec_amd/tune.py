@@ -426,6 +426,7 @@ class TreeModel:
         self.n_features = data["n_features"]
         self.trees = [{k: np.asarray(t[k]) for k in ("left", "right", "feature", "threshold", "value")}
                       for t in data["trees"]]
+        self.report = data.get("report", {})  # held-out quality at training time
         self.best = {}
         for k, v in data.get("best", {}).items():
             f = k.split(",")
