@@ -348,7 +348,10 @@ def train(test_frac=0.2, seed=0, out=MODEL, path=None):
     def fit(rs):
         X = [row_features(r) for r in rs]
         y = [math.log(max(r["ms"], 1e-6)) for r in rs]
-        return GradientBoostingRegressor(n_estimators=300, max_depth=4, learning_rate=0.05,
+        # The reference's GBR(300, lr 0.05) with trees of depth 6 instead of 4:
+        # on this data set (three 80/20 shape splits) the held-out picks ran
+        # 1.063x of the best config (geomean) against 1.112x with depth 4.
+        return GradientBoostingRegressor(n_estimators=300, max_depth=6, learning_rate=0.05,
                                          random_state=seed).fit(X, y)
 
     model = fit([r for r in rows if _key(r) not in test])
