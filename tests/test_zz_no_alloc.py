@@ -4,7 +4,7 @@ against tilec_matmul with caller-owned scratch, through the C ABI.
 Both run the same kernels on the same inputs, so the outputs must agree bit
 for bit: on two calls in a row that split K (the second one smaller, so the
 static scratch holds the first call's partials when it starts), for the
-streaming, panel and tile-GEMM kernels, fp32 and bf16.
+streaming, panel, direct and tile-GEMM kernels, fp32 and bf16.
 """
 
 import ctypes
@@ -67,6 +67,7 @@ CASES = [
     ("skinny_f32_p_v1_w8", torch.float32, (1, 4096, 4096), (1, 1500, 520), 0),  # panel kernel
     ("skinny_f32_w4_b2", torch.float32, (7, 8192, 1000), (2, 3000, 130), 16),   # streaming, 16 splits
     ("gemm_f32_64x64x16_w2x2", torch.float32, (100, 4096, 200), (65, 2000, 70), 8),  # tile GEMM split K
+    ("direct_f32_32x64_w4_db", torch.float32, (513, 3001, 127), (127, 1000, 513), 7),  # direct kernel, 7 splits
     ("skinny_bf16_p_v1_w8", torch.bfloat16, (1, 4096, 4096), (1, 2048, 264), 0),
     (None, torch.bfloat16, (16, 4096, 4096), (5, 999, 136), 0),
 ]
