@@ -84,6 +84,12 @@ def test_hip_configs_rules():
     assert not ext.direct_regime(2049, 2048, "f32") and not ext.direct_regime(1024, 1024, "bf16")
     assert any(c[0].startswith("direct_") for c in ext.hip_configs(1024, 1024, 1024, "f32"))
     assert not any(c[0].startswith("direct_") for c in ext.hip_configs(4096, 4096, 4096, "f32"))
+    # no direct config past the library's 2 GiB partials limit is offered
+    names = {v["name"]: v for v in _lib.variants()}
+    for M, K, N in [(2048, 4096, 2048), (1024, 1024, 1024), (513, 3001, 127), (1, 65536, 4096)]:
+        for name, s in ext.hip_configs(M, K, N, "f32"):
+            if name.startswith("direct_"):
+                assert ext.direct_workspace_bytes(names[name], M, N, ext._direct_splits(K, s)) < 1 << 31
     for M, K, N, dt in [(1, 4096, 4096, "f32"), (16, 4096, 4096, "f32"), (17, 4096, 4096, "f32"),
                         (4096, 4096, 4096, "f32"), (8192, 8192, 8192, "bf16"), (3, 100, 7, "f32"),
                         (1, 4096, 4096, "bf16"), (1024, 1024, 1024, "f32"), (520, 8192, 1648, "bf16")]:
@@ -130,6 +136,7 @@ def test_direct_split_geometry_matches_the_library():
                 assert eff == ext.cdiv(K, kc) and (eff - 1) * kc < K
                 ws = L.tilec_matmul_workspace_bytes(M, N, K, _lib.F32, v["id"], s)
                 cnt = L.tilec_matmul_counter_bytes(M, N, K, _lib.F32, v["id"], s)
+                assert ws == (ext.direct_workspace_bytes(v, M, N, eff) if eff > 1 else 0)
                 if eff == 1:
                     assert ws == 0 and cnt == 0, (v["name"], M, N, K, s)
                 else:

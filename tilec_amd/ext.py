@@ -112,13 +112,16 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             if not (skinny_regime(M, N, code) or direct_regime(M, N, code)) or v["bm"] >= 2 * max(M, 16):
                 continue
             # Splits that fill the CUs exactly once or twice over are
-            # offered beside the powers of two.
+            # offered beside the powers of two; none whose partials would
+            # reach the library's 2 GiB limit.
             tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
             fills = [f for f in (SMALL_OUTPUT_TILES // tiles, 2 * SMALL_OUTPUT_TILES // tiles) if f > 1]
             seen = set()
             for s in sorted(set(_SKINNY_SPLITS) | set(fills)):
                 eff = _direct_splits(K, s)
                 if eff in seen or (eff > 1 and cdiv(K, eff) < 16 * v["waves"]):
+                    continue
+                if eff > 1 and direct_workspace_bytes(v, M, N, eff) >= 1 << 31:
                     continue
                 seen.add(eff)
                 out.append((v["name"], s))
@@ -218,6 +221,14 @@ def _skinny_splits(K, split_k, kc_max):
     s = max(split_k, 1, cdiv(K, kc_max))
     kc = cdiv(cdiv(K, s), 16) * 16
     return cdiv(K, kc)
+
+
+def direct_workspace_bytes(v, M, N, splits):
+    """Split-K partials of a direct variant (tilec_amd/csrc/direct.hip,
+    direct_workspace_bytes): splits x tiles x (16-byte results per thread
+    after the waves meet) x threads."""
+    items = 4 * (v["bm"] // 16) * (v["bn"] // 64)
+    return splits * cdiv(M, v["bm"]) * cdiv(N, v["bn"]) * cdiv(items, v["waves"]) * v["waves"] * 64 * 16
 
 
 def _direct_splits(K, split_k):
