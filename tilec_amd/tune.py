@@ -74,6 +74,7 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
 
 
 GRAPH_BELOW_MS = 0.2   # calls shorter than this are timed from a replayed HIP graph
+GRAPH_FILL_MS = 2.0    # ... of this much device time per replay (at most 256 calls)
 SUSTAIN_CALLS = 4      # longer calls: back-to-back launches per timed sample
 SUSTAIN_WARMUP = 4     # ... after this many untimed back-to-back launches
 ROTATE_BYTES = 512 << 20  # rotate x2 over copies this large in total (> 256 MB Infinity Cache)
@@ -114,9 +115,10 @@ def time_ms(x1, x2, config, best=None, reps=5, x2s=None):
     exit of tilec/tune.py:35-51 when a probe run is over twice the best.
 
     Device time from HIP events.  A call shorter than GRAPH_BELOW_MS is timed
-    as a replay of a captured HIP graph of several calls (cycling over `x2s`
-    when given), so host launch overhead does not pollute it; the result is
-    the median replay time divided by the calls per replay.  Longer calls
+    as a replay of a captured HIP graph of enough calls to fill about
+    GRAPH_FILL_MS (cycling over `x2s` when given), so neither host launch
+    overhead nor the replay's start-up pollutes it; the result is the median
+    replay time divided by the calls per replay.  Longer calls
     are timed as SUSTAIN_CALLS back-to-back launches per sample, after
     SUSTAIN_WARMUP more, i.e. at the clock the chip holds under load."""
     import torch
@@ -136,7 +138,11 @@ def time_ms(x1, x2, config, best=None, reps=5, x2s=None):
     if best is not None and first >= GRAPH_BELOW_MS and first > 2 * best:
         return first
     if first < GRAPH_BELOW_MS:
-        calls = max(8, len(x2s))
+        # Enough calls per replay to fill about GRAPH_FILL_MS of device time
+        # (a multiple of the x2 copies): a replay's start-up costs a few us,
+        # which a handful of GEMV-sized calls would each carry about 1 us of.
+        n = max(8, len(x2s), min(256, math.ceil(GRAPH_FILL_MS / max(first, 1e-3))))
+        calls = math.ceil(n / len(x2s)) * len(x2s)
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
         graph = torch.cuda.CUDAGraph()
