@@ -42,17 +42,21 @@ struct GemmF32 {
   static constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
   static_assert(BK % 8 == 0, "BK: whole 8-deep k chunks");
-  // K chunk (8 deep: four MFMA k-pairs) after whose MFMAs the next tile goes
-  // from registers to LDS.  With enough MFMAs per step the store sits
-  // mid-step, where its LDS writes overlap the matrix cores and the step's
-  // global loads have long arrived; short steps store at the end, after the
-  // MFMAs have covered the loads.
+  // K chunk (8 deep: four MFMA k-pairs) before whose MFMAs the next tile goes
+  // from registers to LDS; its loads were issued a step earlier.  Storing
+  // early leaves the LDS writes the rest of the step to complete under the
+  // matrix cores: waves with at least 96 MFMAs per step (the 256 x 256
+  // tiles) store after their first chunk, other 8-wave tiles mid-step (at
+  // 4096^3 and 2048^3 these beat every other
+  // position: chunk 0 waits for loads still in flight, later positions
+  // leave the writes less cover).  4-wave tiles run two workgroups per CU,
+  // whose barriers interleave, and store at the end of the step.
   // Waves per SIMD the register budget is held to: 4-wave workgroups with
   // at most 128 accumulators per lane fit two workgroups per CU, whose
   // barriers are independent, so one's MFMAs cover the other's waits.
   static constexpr int kWavesPerSimd = (WM * WN == 4 && TM * TN * 16 <= 128) ? 2 : 1;
   static constexpr int KS = BK / 8;
-  static constexpr int kStoreAt = TM * TN * BK / 2 >= 96 ? KS / 2 : KS;
+  static constexpr int kStoreAt = TM * TN * BK / 2 >= 96 ? 1 : (WM * WN == 8 ? KS / 2 : KS);
 };
 
 // Four consecutive floats at a 4-byte aligned address: one dwordx4 load,
@@ -151,12 +155,16 @@ struct OperandF32 {
   // !VEC) a select that clears the columns past the edge inside the quad that
   // straddles it.  Otherwise MASK selects clamped, per-element loads at
   // every edge and unmasked 16-byte loads elsewhere.
+  // `live` false (BUF only): the tile lies past this workgroup's K range;
+  // its loads still issue, through an empty resource (zeros, no traffic), so
+  // every step issues the same loads and the compiler's wait before the LDS
+  // store counts only the loads that store needs.
   template <int SET>
-  __device__ __forceinline__ void load(int kt, bool mask) {
+  __device__ __forceinline__ void load(int kt, bool mask, bool live = true) {
     const int k0 = kt * BK;
     if constexpr (BUF) {
-      const BufRsrc rs = KC ? make_rsrc(X + (int64_t)r0 * ld + k0, extent(Rtot - r0, ld, K - k0))
-                            : make_rsrc(X + (int64_t)k0 * ld + r0, extent(K - k0, ld, Rtot - r0));
+      const uint32_t n = KC ? extent(Rtot - r0, ld, K - k0) : extent(K - k0, ld, Rtot - r0);
+      const BufRsrc rs = make_rsrc(X + (KC ? (int64_t)r0 * ld + k0 : (int64_t)k0 * ld + r0), live ? n : 0u);
 #pragma unroll
       for (int p = 0; p < Q; ++p) {
         f32x4 x = load_f32x4(rs, k0 + tk[p] < K ? off[p] : kOob);
@@ -237,9 +245,9 @@ __global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesP
   opb.init(B, ldb, n0, N, K, tid);
   // Tile t (counted from kt0) moves through register set t % 2 and LDS
   // buffer t % 2.
-  auto gload = [&](auto set, int kt, bool mask) {
-    opa.template load<decltype(set)::value>(kt, mask);
-    opb.template load<decltype(set)::value>(kt, mask);
+  auto gload = [&](auto set, int kt, bool mask, bool live = true) {
+    opa.template load<decltype(set)::value>(kt, mask, live);
+    opb.template load<decltype(set)::value>(kt, mask, live);
   };
   auto sstore = [&](auto set) {
     constexpr int T = decltype(set)::value;
@@ -278,7 +286,10 @@ __global__ __launch_bounds__(WM * WN * 64, (GemmF32<BM, BN, BK, WM, WN>::kWavesP
   auto step = [&](int kt, auto par) __attribute__((always_inline)) {
     constexpr int T = decltype(par)::value;
     using Next = std::integral_constant<int, T ^ 1>;
-    if (kt + 2 < kt1) gload(par, kt + 2, !(interior && kt + 2 < nk_full));
+    if (BUF)
+      gload(par, kt + 2, false, kt + 2 < kt1);
+    else if (kt + 2 < kt1)
+      gload(par, kt + 2, !(interior && kt + 2 < nk_full));
     const float* as = As + T * OpA::STAGE;
     const float* bs = Bs + T * OpB::STAGE;
 #pragma unroll
@@ -410,6 +421,8 @@ const VariantDesc* gemm_f32_variants(int* count) {
        launch_gemm_f32<128, 128, 32, 2, 4>},
       {"gemm_f32_128x128x32_w2x2", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 32, 4, 0, 1,
        launch_gemm_f32<128, 128, 32, 2, 2>},
+      {"gemm_f32_128x128x64_w2x4", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 64, 8, 0, 1,
+       launch_gemm_f32<128, 128, 64, 2, 4>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;
