@@ -319,10 +319,33 @@ CONFIG_CASES = (
 )
 
 
+def _graph_ms(fn, reps):
+    """ms per call of fn() from replays of a HIP graph of `reps` calls, after
+    SETTLE_MS / 2 of untimed replays."""
+    import torch
+    fn()  # workspace exists before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            outs = [fn() for _ in range(reps)]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        ms = timed(g.replay, 3, 1, stream=s, settle_ms=SETTLE_MS / 2) / reps
+    del outs
+    return ms
+
+
 def bench_configs(reps=20):
     """Every fp32 BASELINE config: device time per call from a HIP graph of
     `reps` calls (so small, latency-bound shapes are not timed as host
-    overhead), TFLOP/s and the fraction of the fp32 matrix peak."""
+    overhead), TFLOP/s and the fraction of the fp32 matrix peak; beside it
+    the vendor's torch.mm (hipBLASLt / rocBLAS) on the same inputs, timed the
+    same way."""
     import torch
     from oracle import oracle as O
     from tilec_amd import ext
@@ -334,24 +357,15 @@ def bench_configs(reps=20):
         x1 = torch.from_numpy(draw((M, K), 100 + 2 * i)).cuda()
         x2 = torch.from_numpy(draw((K, N), 101 + 2 * i)).cuda()
         cfg = kernel_name_for(M, K, N, "f32")
-        ext.matrix_mul(x1, x2)  # workspace exists before capture
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            ext.matrix_mul(x1, x2)
-            torch.cuda.synchronize()
-            with torch.cuda.graph(g, stream=s):
-                outs = [ext.matrix_mul(x1, x2) for _ in range(reps)]
-        torch.cuda.synchronize()
-        with torch.cuda.stream(s):
-            ms = timed(g.replay, 3, 1, stream=s, settle_ms=SETTLE_MS / 2) / reps
-        del outs
+        ms = _graph_ms(lambda: ext.matrix_mul(x1, x2), reps)
         tflops = 2 * M * N * K / (ms * 1e-3) / 1e12
+        vendor_ms = _graph_ms(lambda: torch.mm(x1, x2), reps) if CASE is None else None
         out[name] = dict(us=ms * 1e3, TFLOPs=tflops, frac=tflops / PEAK_FP32_MFMA, config=list(cfg),
-                         traffic=traffic_of(cfg[0], M, N, K))
-        log(f"{name}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s ({cfg})")
+                         traffic=traffic_of(cfg[0], M, N, K),
+                         torch_mm_us=vendor_ms and vendor_ms * 1e3,
+                         speedup_vs_torch_mm=vendor_ms and vendor_ms / ms)
+        log(f"{name}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s ({cfg})"
+            + (f"; torch.mm {vendor_ms * 1e3:.1f} us" if vendor_ms else ""))
     return out
 
 
