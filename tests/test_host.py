@@ -110,7 +110,7 @@ def test_hip_configs_rules():
             else:
                 tiles = ext.cdiv(M, v["bm"]) * ext.cdiv(N, v["bn"])
                 eff = ext._gemm_splits(K, s, v["bk"])
-                assert eff == 1 or (ext.tile_can_split(v) and tiles < ext.SMALL_OUTPUT_TILES
+                assert eff == 1 or (ext.tile_can_split(v) and tiles < ext.device_cus()
                                     and ext.cdiv(K, v["bk"]) >= 4 * eff)
         has_skinny = any(names[n]["family"] == _lib.FAMILY_SKINNY for n, _ in cfgs)
         assert has_skinny == ext.skinny_regime(M, N, dt)

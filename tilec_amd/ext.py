@@ -115,7 +115,7 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             # offered beside the powers of two; none whose partials would
             # reach the library's 2 GiB limit.
             tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
-            fills = [f for f in (SMALL_OUTPUT_TILES // tiles, 2 * SMALL_OUTPUT_TILES // tiles) if f > 1]
+            fills = [f for f in (device_cus() // tiles, 2 * device_cus() // tiles) if f > 1]
             seen = set()
             for s in sorted(set(_SKINNY_SPLITS) | set(fills)):
                 eff = _direct_splits(K, s)
@@ -139,7 +139,7 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
         else:
             out.append((v["name"], 1))
             tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
-            if tiles < SMALL_OUTPUT_TILES and tile_can_split(v):
+            if tiles < device_cus() and tile_can_split(v):
                 seen = {1}
                 for s in _GEMM_SPLITS:
                     eff = _gemm_splits(K, s, v["bk"])
@@ -192,7 +192,18 @@ def _gemm_splits(K, split_k, bk):
     return cdiv(total, steps)
 
 
-SMALL_OUTPUT_TILES = 256  # MI355X CUs: 64x64 output tiles below this leave CUs idle
+_CUS = None
+
+
+def device_cus():
+    """CUs of the current GPU, read once (the library's own rule reads the
+    same count); 64x64 output tiles below this count leave CUs idle.  256, an
+    MI355X's count, where no GPU is visible (host-side tests)."""
+    global _CUS
+    if _CUS is None:
+        _CUS = (torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+                if torch.cuda.is_available() else 256)
+    return _CUS
 
 
 def skinny_regime(M, N, dtype="f32"):
@@ -202,7 +213,7 @@ def skinny_regime(M, N, dtype="f32"):
     16 rows the bf16 tile GEMMs (with a K split) serve them better."""
     if M <= 16:
         return True
-    return _dtype_code_name(dtype) == _lib.F32 and cdiv(M, 64) * cdiv(N, 64) < SMALL_OUTPUT_TILES
+    return _dtype_code_name(dtype) == _lib.F32 and cdiv(M, 64) * cdiv(N, 64) < device_cus()
 
 
 def direct_regime(M, N, dtype="f32"):
@@ -211,7 +222,7 @@ def direct_regime(M, N, dtype="f32"):
     (1024^2 .. 2048^2-sized), where the tile GEMMs' large tiles leave CUs
     idle or need a K split and the direct kernel's 32x64 tiles (two register
     sets of operands in flight) fill the chip unsplit."""
-    return _dtype_code_name(dtype) == _lib.F32 and cdiv(M, 64) * cdiv(N, 64) <= 4 * SMALL_OUTPUT_TILES
+    return _dtype_code_name(dtype) == _lib.F32 and cdiv(M, 64) * cdiv(N, 64) <= 4 * device_cus()
 
 
 def _skinny_splits(K, split_k, kc_max):
