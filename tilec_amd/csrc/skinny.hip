@@ -378,6 +378,20 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(
             accv[m][cc / 4][cc % 4] = __builtin_fmaf(a, b, accv[m][cc / 4][cc % 4]);
           }
         }
+    } else if constexpr (!CB && CPL == 8) {
+      // bf16: the lane's rows 4r + u (u < 4) of column col + c are the B
+      // operand of a 16x16x16 bf16 MFMA (k = 4r + u) and x1[q][4r .. 4r+3]
+      // its A operand, so a block is CPL MFMAs on bf16 pairs packed by byte
+      // permutes, with no widening to fp32.
+      //   D_c[m][q] += sum_{r,u} x1[m][4r+u] * x2[4r+u][col + c]
+      const s16x4 a = __builtin_bit_cast(s16x4, blk.a);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const unsigned sel = (c & 1) ? 0x07060302u : 0x05040100u;  // high or low halves of two dwords
+        const int lo = (int)__builtin_amdgcn_perm((unsigned)blk.b[1][c >> 1], (unsigned)blk.b[0][c >> 1], sel);
+        const int hi = (int)__builtin_amdgcn_perm((unsigned)blk.b[3][c >> 1], (unsigned)blk.b[2][c >> 1], sel);
+        acc[c] = mfma16x16x16bf16(a, __builtin_bit_cast(s16x4, i32x2{lo, hi}), acc[c]);
+      }
     } else if constexpr (!CB) {
       // D_c[m][q] += sum_r x1[m][4r+u] * x2[4r+u][col + c]
 #pragma unroll
