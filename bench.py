@@ -287,7 +287,12 @@ def bench_vendor(steps=200):
     b = torch.from_numpy(O.normal((n, n), 9, std=sigma)).to(torch.bfloat16).cuda()
     ms = timed(lambda: _vendor_mm(a, b), 20, 2, settle_ms=SETTLE_MS)
     out["bf16_8192"] = dict(ms=ms, TFLOPs=2 * n ** 3 / (ms * 1e-3) / 1e12)
-    del a, b
+    # x2 column-major (both operands k-contiguous), beside the library's
+    # layouts section figure for the same layout
+    bt = b.t().contiguous().t()
+    ms = timed(lambda: _vendor_mm(a, bt), 20, 2, settle_ms=SETTLE_MS)
+    out["bf16_8192_x2T"] = dict(ms=ms, TFLOPs=2 * n ** 3 / (ms * 1e-3) / 1e12)
+    del a, b, bt
     K = N = 4096
     for dtype, Ms in (("f32", (1, 16)), ("bf16", (1, 16))):
         tdt = torch.float32 if dtype == "f32" else torch.bfloat16
