@@ -33,6 +33,9 @@
 
 namespace tilec {
 
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB>
+hipError_t launch_gemm_f32_lds(const MatmulArgs& a);  // gemm_f32_lds.hip
+
 namespace {
 
 template <int BM, int BN, int BK, int WM, int WN>
@@ -378,6 +381,32 @@ hipError_t launch_layout(const MatmulArgs& a) {
              : launch_one<BM, BN, BK, WM, WN, false, false, CA, CB>(a, grid);
 }
 
+// Aligned operands (16-byte bases, contiguous extents and strides multiples
+// of 4) whose per-step offsets fit 32 bits run the LDS-DMA kernel of
+// gemm_f32_lds.hip with a ring of NBUF stage buffers; everything else runs
+// the register-staged kernel above with the same tile and waves.
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB>
+hipError_t launch_layout_lds(const MatmulArgs& a) {
+  const int64_t a_run = CA ? a.M : a.K, b_run = CB ? a.K : a.N;
+  const bool vec = (a_run % 4 == 0) && (b_run % 4 == 0) && (a.ldx1 % 4 == 0) && (a.ldx2 % 4 == 0) &&
+                   (reinterpret_cast<uintptr_t>(a.x1) % 16 == 0) && (reinterpret_cast<uintptr_t>(a.x2) % 16 == 0);
+  const int64_t a_rows = CA ? BK : BM, b_rows = CB ? BN : BK;
+  constexpr int64_t lim = (int64_t(1) << 31) - 4096;
+  if (vec && a_rows * a.ldx1 * 4 < lim && b_rows * a.ldx2 * 4 < lim)
+    return launch_gemm_f32_lds<BM, BN, BK, NBUF, WM, WN, CA, CB>(a);
+  return launch_layout<BM, BN, BK, WM, WN, CA, CB>(a);
+}
+
+template <int BM, int BN, int BK, int NBUF, int WM, int WN>
+hipError_t launch_gemm_f32_dma(const MatmulArgs& a) {
+  switch (a.layout & 3) {
+    case 0: return launch_layout_lds<BM, BN, BK, NBUF, WM, WN, false, false>(a);
+    case TILEC_X1_COL_MAJOR: return launch_layout_lds<BM, BN, BK, NBUF, WM, WN, true, false>(a);
+    case TILEC_X2_COL_MAJOR: return launch_layout_lds<BM, BN, BK, NBUF, WM, WN, false, true>(a);
+    default: return launch_layout_lds<BM, BN, BK, NBUF, WM, WN, true, true>(a);
+  }
+}
+
 template <int BM, int BN, int BK, int WM, int WN>
 hipError_t launch_gemm_f32(const MatmulArgs& a) {
   switch (a.layout & 3) {
@@ -423,6 +452,13 @@ const VariantDesc* gemm_f32_variants(int* count) {
        launch_gemm_f32<128, 128, 32, 2, 2>},
       {"gemm_f32_128x128x64_w2x4", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 64, 8, 0, 1,
        launch_gemm_f32<128, 128, 64, 2, 4>},
+      // direct-to-LDS copies (gemm_f32_lds.hip); unroll = ring depth
+      {"gemm_f32_256x256x32_w2x4_lds", TILEC_FAMILY_GEMM, TILEC_F32, 256, 256, 32, 8, 0, 2,
+       launch_gemm_f32_dma<256, 256, 32, 2, 2, 4>},
+      {"gemm_f32_128x128x32_w2x4_lds", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 32, 8, 0, 3,
+       launch_gemm_f32_dma<128, 128, 32, 3, 2, 4>},
+      {"gemm_f32_128x128x64_w2x4_lds", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 64, 8, 0, 2,
+       launch_gemm_f32_dma<128, 128, 64, 2, 2, 4>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

@@ -178,8 +178,10 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
     // geometric mean; the tile GEMMs below alone: 1.37x).
     if (cdiv(M, 128) * cdiv(N, 128) < cus && cdiv(M, 64) * cdiv(N, 64) <= 4 * (int64_t)cus)
       return find("direct_f32_32x64_w4_db");
-    static const char* order[] = {"gemm_f32_256x256x32_w2x4", "gemm_f32_256x128x16_w2x2",
-                                  "gemm_f32_128x128x32_w2x4", "gemm_f32_128x64x16_w2x2"};
+    // (the *_lds tiles run the register-staged kernel of the same tile for
+    // operands their direct-to-LDS copies do not take)
+    static const char* order[] = {"gemm_f32_256x256x32_w2x4_lds", "gemm_f32_256x128x16_w2x2",
+                                  "gemm_f32_128x128x32_w2x4_lds", "gemm_f32_128x64x16_w2x2"};
     for (const char* nm : order) {
       const int v = find(nm);
       const VariantDesc* d = table()[v];
