@@ -459,6 +459,10 @@ const VariantDesc* gemm_f32_variants(int* count) {
        launch_gemm_f32_dma<128, 128, 32, 3, 2, 4>},
       {"gemm_f32_128x128x64_w2x4_lds", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 64, 8, 0, 2,
        launch_gemm_f32_dma<128, 128, 64, 2, 2, 4>},
+      {"gemm_f32_64x64x32_w2x2_lds", TILEC_FAMILY_GEMM, TILEC_F32, 64, 64, 32, 4, 0, 3,
+       launch_gemm_f32_dma<64, 64, 32, 3, 2, 2>},
+      {"gemm_f32_64x64x64_w2x2_lds", TILEC_FAMILY_GEMM, TILEC_F32, 64, 64, 64, 4, 0, 3,
+       launch_gemm_f32_dma<64, 64, 64, 3, 2, 2>},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

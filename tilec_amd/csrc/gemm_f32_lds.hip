@@ -391,6 +391,8 @@ hipError_t launch_gemm_f32_lds(const MatmulArgs& a) {
 TILEC_F32_LDS_VARIANT(256, 256, 32, 2, 2, 4)
 TILEC_F32_LDS_VARIANT(128, 128, 32, 3, 2, 4)
 TILEC_F32_LDS_VARIANT(128, 128, 64, 2, 2, 4)
+TILEC_F32_LDS_VARIANT(64, 64, 32, 3, 2, 2)
+TILEC_F32_LDS_VARIANT(64, 64, 64, 3, 2, 2)
 #undef TILEC_F32_LDS_VARIANT
 
 }  // namespace tilec
