@@ -407,8 +407,10 @@ def test_select_variant_rules():
     names = [v["name"] for v in _lib.variants()]
     assert names[L.tilec_select_variant(1, 4096, 4096, 0)].startswith("skinny_f32")
     assert names[L.tilec_select_variant(4096, 4096, 4096, 0)].startswith("gemm_f32")
-    # medium fp32 outputs: the direct kernel's two-register-set 32x64 tile, unless 128x128 tiles fill the CUs
-    assert names[L.tilec_select_variant(1024, 1024, 1024, 0)] == "direct_f32_32x64_w4_db"
+    # medium fp32 outputs: the direct-to-LDS 64x64 tile where its tiles give each CU one or two, else the
+    # direct kernel's two-register-set 32x64 tile, unless 128x128 tiles fill the CUs
+    assert names[L.tilec_select_variant(1024, 1024, 1024, 0)] == "gemm_f32_64x64x32_w2x2_lds"
+    assert names[L.tilec_select_variant(3001, 1000, 513, 0)] == "direct_f32_32x64_w4_db"  # M, N, K
     assert names[L.tilec_select_variant(2048, 2048, 2048, 0)].startswith("gemm_f32")
     assert names[L.tilec_select_variant(8192, 8192, 8192, 1)].startswith("gemm_bf16")
     assert names[L.tilec_select_variant(4, 4096, 4096, 1)].startswith("skinny_bf16")
