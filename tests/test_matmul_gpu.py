@@ -604,6 +604,43 @@ def test_bf16_variant_layouts(name):
                 assert O.rel_l2(got, ref) <= 1e-5, (name, layout, s, (m, k, n))
 
 
+def test_f32_lds_copies_strides_and_fallbacks():
+    """The fp32 tiles with direct-to-LDS copies (*_lds) against the fp64
+    oracle and, where the library has one, the register-staged variant of
+    the same tile, bit for bit: row strides padded to a multiple of 4 (the copies' path), strides
+    and bases that are not (a flat[1:] view, a stride of N + 3: the
+    register-staged fallback), K tails, partial edge tiles, every layout, and
+    K splits for the tiles that split."""
+    lds = [v for v in _lib.variants() if v["name"].endswith("_lds")]
+    assert len(lds) == 5
+    names = {v["name"] for v in _lib.variants()}
+    shapes = [(256, 512, 256), (300, 260, 196), (130, 1004, 72), (64, 32, 64), (520, 4100, 264)]
+    for i, (m, k, n) in enumerate(shapes):
+        a, b = O.normal((m, k), 1300 + 2 * i), O.normal((k, n), 1301 + 2 * i)
+        ref = O.matmul_f64(a, b)
+        fa = torch.zeros(m * k + 1, device="cuda")
+        fa[1:] = dev(a).flatten()
+        views = {"aligned": (dev(a), dev(b)), "unaligned x1 base": (fa[1:].view(m, k), dev(b))}
+        for v in lds:
+            base = v["name"][:-4]
+            splits = [1, 3] if ext.tile_can_split(v) else [1]
+            for s in splits:
+                for label in ("aligned", "unaligned x1 base"):
+                    x1, x2 = views[label]
+                    say(f"{v['name']} split {s} {label} shape {(m, k, n)}")
+                    got = ext.matrix_mul(x1, x2, (v["name"], s))
+                    if base in names:  # the 64x64 tiles have no register-staged variant of their own
+                        assert torch.equal(got, ext.matrix_mul(x1, x2, (base, s))), (v["name"], s, label, (m, k, n))
+                    assert O.rel_l2(got.cpu().numpy(), ref) <= O.TOL_F32, (v["name"], s, label, (m, k, n))
+                for layout in [0] + LAYOUTS:
+                    for pad in (4, 3):
+                        say(f"{v['name']} split {s} layout {layout} pad {pad} shape {(m, k, n)}")
+                        got = run_layout(dev(a), dev(b), layout, (v["name"], s), pad=pad)
+                        if base in names:
+                            np.testing.assert_array_equal(got, run_layout(dev(a), dev(b), layout, (base, s), pad=pad))
+                        assert O.rel_l2(got, ref) <= O.TOL_F32, (v["name"], s, layout, pad, (m, k, n))
+
+
 def test_layouts_padded_strides_and_splits():
     """Column strides above the row count, and K splits of the tile GEMMs,
     in every layout."""
