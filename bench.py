@@ -69,7 +69,7 @@ def parse():
                    help="with --only skinny, configs or reduce: run only the cases whose key contains this "
                         "text (one kernel per profile run)")
     p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "vendor", "copy",
-                                      "host", "tuner", "cpu"],
+                                      "host", "tuner", "cpu", "ksweep"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -478,6 +478,36 @@ def bench_tuner():
                 cases=cases, held_out_report=getattr(model, "report", None))
 
 
+def bench_ksweep(ks=(4096, 8192, 16384), rounds=3):
+    """fp32 4096 x K x 4096 for growing K, through the kernel the library
+    picks at 4096^3 and through torch.mm, medians of `rounds` timings in one process: the change in time
+    per added 4096 of K is the K loop's steady state, the rest the fixed cost
+    of a launch (prologue, epilogue, imbalance across CUs)."""
+    import torch
+    from oracle import oracle as O
+    from tilec_amd import ext
+    n, out = 4096, {}
+    cfg = kernel_name_for(n, n, n, "f32")  # one kernel for every K: the 4096^3 pick
+    for K in ks:
+        a = torch.from_numpy(O.uniform((n, K), 4)).cuda()
+        b = torch.from_numpy(O.uniform((K, n), 5)).cuda()
+        mine = sorted(timed(lambda: ext.matrix_mul(a, b, cfg), 10, 2, settle_ms=SETTLE_MS) for _ in range(rounds))
+        vend = sorted(timed(lambda: _vendor_mm(a, b), 10, 2, settle_ms=SETTLE_MS) for _ in range(rounds))
+        flops = 2 * n * n * K
+        out[f"K{K}"] = dict(ms=mine[rounds // 2], frac=flops / (mine[rounds // 2] * 1e-3) / 1e12 / PEAK_FP32_MFMA,
+                            config=list(cfg), torch_mm_ms=vend[rounds // 2])
+        log(f"4096x{K}x4096: {mine[rounds // 2]:.4f} ms ({cfg[0]}), torch.mm {vend[rounds // 2]:.4f} ms")
+        del a, b
+    k0, k1 = ks[0], ks[-1]
+    per = (out[f"K{k1}"]["ms"] - out[f"K{k0}"]["ms"]) / ((k1 - k0) / 4096)
+    per_v = (out[f"K{k1}"]["torch_mm_ms"] - out[f"K{k0}"]["torch_mm_ms"]) / ((k1 - k0) / 4096)
+    t4096 = 2 * n ** 3 / (PEAK_FP32_MFMA * 1e12) * 1e3
+    out["steady_state"] = dict(ms_per_4096_k=per, frac=t4096 / per, fixed_ms=out[f"K{k0}"]["ms"] - per * k0 / 4096,
+                               torch_mm_ms_per_4096_k=per_v, torch_mm_frac=t4096 / per_v,
+                               torch_mm_fixed_ms=out[f"K{k0}"]["torch_mm_ms"] - per_v * k0 / 4096)
+    return out
+
+
 def bench_copy(nbytes=256 << 20, reps=10):
     """A plain device-to-device copy of known size: what FETCH_SIZE and
     WRITE_SIZE read for it calibrates those counters."""
@@ -659,6 +689,7 @@ def main():
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
                "configs": bench_configs, "layouts": bench_layouts, "reduce": bench_reduce,
                "vendor": bench_vendor, "copy": bench_copy, "host": bench_host, "tuner": bench_tuner,
+               "ksweep": bench_ksweep,
                "cpu": lambda: bench_cpu(args.cpu_seconds)}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return
