@@ -188,6 +188,10 @@ CONFIG_SHAPES = [
     (127, 1000, 513, "f32"), (513, 3001, 127, "f32"), (1000, 4097, 3001, "f32"), (3001, 513, 1000, "f32"),
     (8192, 8192, 8192, "bf16"), (4096, 4096, 4096, "bf16"),
     (1, 4096, 4096, "bf16"), (16, 4096, 4096, "bf16"),
+    # large outputs with long K, past the generator's range, so the model does
+    # not extrapolate small tiles there
+    (4096, 8192, 4096, "f32"), (4096, 16384, 4096, "f32"), (2048, 16384, 2048, "f32"), (8192, 4096, 8192, "f32"),
+    (3072, 12288, 3072, "f32"), (8192, 8192, 4096, "bf16"),
 ]
 # The same sizes with transposed operands (x @ W.T GEMV, TN / NT / TT GEMMs).
 LAYOUT_CONFIG_SHAPES = [
