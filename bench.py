@@ -119,7 +119,7 @@ def timed(fn, steps, warmup, stream=None, settle_ms=0.0):
 
 
 def kernel_name_for(M, K, N, dtype, layout=0):
-    from tilec_amd import _lib, tune
+    from tilec import _lib, tune
     p = tune.pick(M, K, N, dtype, layout)
     if p is not None:
         return p
@@ -132,7 +132,7 @@ def kernel_name_for(M, K, N, dtype, layout=0):
 def bench_square(args):
     import torch
     from oracle import oracle as O  # seeded generators only
-    from tilec_amd import ext
+    from tilec import ext
     n = 4096
     a = torch.from_numpy(O.uniform((n, n), 4)).cuda()
     b = torch.from_numpy(O.uniform((n, n), 5)).cuda()
@@ -148,7 +148,7 @@ def _gemv(x1, x2s, steps, mm=None, settle_ms=0.0):
     x2 buffers, launches replayed from a HIP graph (an ~8 us kernel is not
     host-bound), after `settle_ms` of untimed replays."""
     import torch
-    from tilec_amd import ext
+    from tilec import ext
     mm = mm or ext.matrix_mul
     nbuf = len(x2s)
     for i in range(nbuf):  # warm up: workspace exists before capture
@@ -181,7 +181,7 @@ def _gemv_cases(ms_by_dtype, transposed, steps):
     serves a repeat."""
     import torch
     from oracle import oracle as O
-    from tilec_amd import ext
+    from tilec import ext
     K = N = 4096
     out = {}
     for dtype, Ms in ms_by_dtype:
@@ -221,7 +221,7 @@ def bench_layouts(steps=200, gemm_steps=20):
     bf16 8192^3 GEMMs with x1, x2 or both column-major."""
     import torch
     from oracle import oracle as O
-    from tilec_amd import ext
+    from tilec import ext
     out = {"gemv_x_WT": _gemv_cases((("f32", (1, 16)), ("bf16", (1, 16))), True, steps)}
     for dtype, n, peak in (("f32", 4096, PEAK_FP32_MFMA), ("bf16", 8192, PEAK_BF16_MFMA)):
         if CASE is not None and not CASE.startswith(f"{dtype}_{n}"):
@@ -246,7 +246,7 @@ def bench_layouts(steps=200, gemm_steps=20):
 def bench_bf16(steps=20, warmup=2):
     import torch
     from oracle import oracle as O
-    from tilec_amd import ext
+    from tilec import ext
     n = 8192
     sigma = n ** -0.25
     a = torch.from_numpy(O.normal((n, n), 8, std=sigma)).to(torch.bfloat16).cuda()
@@ -353,7 +353,7 @@ def bench_configs(reps=20):
     same way."""
     import torch
     from oracle import oracle as O
-    from tilec_amd import ext
+    from tilec import ext
     out = {}
     for i, (name, M, K, N, gen) in enumerate(CONFIG_CASES):
         if CASE is not None and CASE not in name:
@@ -392,7 +392,7 @@ def bench_reduce(reps=8):
     accumulate and out) timed the same way."""
     import torch
     from oracle import oracle as O
-    from tilec_amd import ext
+    from tilec import ext
     out = {}
     for i, (name, R, C, dtype, axis) in enumerate(REDUCE_CASES):
         if CASE is not None and CASE not in name:
@@ -433,7 +433,7 @@ def bench_reduce(reps=8):
     return out
 
 
-# Shapes absent from the tuner's timing table (tilec_amd/mm_bench_mi355x.csv),
+# Shapes absent from the tuner's timing table (tilec/mm_bench_mi355x.csv),
 # one or more per regime: GEMV, small output, medium, large fp32 and bf16.
 TUNER_UNSEEN = [(5, 3000, 2500, "f32"), (12, 6000, 1000, "bf16"), (48, 2900, 1800, "f32"), (96, 4000, 640, "f32"),
                 (200, 1500, 3000, "f32"), (777, 777, 777, "f32"), (1500, 3100, 900, "f32"),
@@ -447,7 +447,7 @@ def bench_tuner():
     protocol (`tune.time_ms`, x2 rotated as in its table), beside the
     held-out report stored with the model."""
     import torch
-    from tilec_amd import tune, ext
+    from tilec import tune, ext
     model = tune._model()
     g = torch.Generator(device="cuda").manual_seed(0)
     cases = []
@@ -485,7 +485,7 @@ def bench_ksweep(ks=(4096, 8192, 16384), rounds=3):
     of a launch (prologue, epilogue, imbalance across CUs)."""
     import torch
     from oracle import oracle as O
-    from tilec_amd import ext
+    from tilec import ext
     n, out = 4096, {}
     cfg = kernel_name_for(n, n, n, "f32")  # one kernel for every K: the 4096^3 pick
     for K in ks:
@@ -627,7 +627,7 @@ def bench_host(calls=2000):
     output allocation, no launch)."""
     import torch
     from oracle import oracle as O
-    from tilec_amd import ext
+    from tilec import ext
     out = {}
     for i, (name, M, K, N) in enumerate(HOST_CASES):
         x1 = torch.from_numpy(O.normal((M, K), 300 + i)).cuda()
@@ -679,7 +679,7 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm GPU visible"}), flush=True)
         sys.exit(1)
-    from tilec_amd import _lib
+    from tilec import _lib
     _lib.lib()  # fail loudly if the HIP library is missing
     props = torch.cuda.get_device_properties(0)
 

@@ -8,7 +8,7 @@
  * goes through `JITFunction.run` / `_launch` (tilec/jit.py:81-105) into
  * `torch.mps.compile_shader(...)(*buffers, threads=..., group_size=...)`.
  * Every entry point below replaces a piece of that path; the Python caller is
- * tilec_amd/ext.py (via ctypes), which keeps the reference's public signature
+ * tilec/ext.py (via ctypes), which keeps the reference's public signature
  * `matrix_mul(x1, x2)` (tilec/ext.py:66-67).
  *
  * Conventions shared by all entry points
@@ -147,7 +147,7 @@ int tilec_matmul_noalloc(const void* x1, const void* x2, float* out,
  * operands row-major and contiguous (what TILEC_VARIANT_AUTO runs for layout
  * 0), or a negative status.  The reference's equivalent is the fixed
  * BM=BN=64, BK=16 default of `_matrix_mul_tiled` (tilec/ext.py:54); the
- * trained per-shape choice lives host-side in tilec_amd/tune.py, as
+ * trained per-shape choice lives host-side in tilec/tune.py, as
  * `tune.pick` does in the reference (tilec/tune.py:143-151).
  */
 int32_t tilec_select_variant(int64_t M, int64_t N, int64_t K, int32_t dtype);

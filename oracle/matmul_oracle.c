@@ -3,7 +3,7 @@
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
  * load this library, and only as the checker (or the timed CPU baseline);
- * the product path (tilec_amd) never calls it and has no CPU fallback.
+ * the product path (the tilec package) never calls it and has no CPU fallback.
  *
  * What it restates
  *   oracle_matmul_tiled_f32  — the reference tile kernel `_matmul_tiled`

@@ -2,7 +2,7 @@
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
 this module, and only as the checker (or the timed CPU baseline).  The product
-(tilec_amd) never imports it.
+(tilec) never imports it.
 
 Contents
   * numpy wrappers of liboracle.so (matmul_oracle.c): the literal tiled

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tilec_amd import _lib, ext, tune
+from tilec import _lib, ext, tune
 import tilec
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tilec_amd import _lib, ext
+from tilec import _lib, ext
 import tilec
 
 pytestmark = pytest.mark.gpu

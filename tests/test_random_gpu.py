@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tilec_amd import ext
+from tilec import ext
 
 pytestmark = pytest.mark.gpu
 

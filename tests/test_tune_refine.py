@@ -2,7 +2,7 @@
 timing CSV (the GPU timing itself is replaced by a script)."""
 import csv
 
-from tilec_amd import tune
+from tilec import tune
 
 ROWS = [
     # shape A: two configs within 10 % of the best, one far behind

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tilec_amd import _lib
+from tilec import _lib
 
 pytestmark = pytest.mark.gpu
 

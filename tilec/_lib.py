@@ -52,7 +52,7 @@ def lib():
     """Load libtilec_hip.so once; raise if it has not been built."""
     if not os.path.exists(LIB_PATH):
         raise LibraryMissing(
-            f"{LIB_PATH} is not built; run `python -m tilec_amd.build` "
+            f"{LIB_PATH} is not built; run `python -m tilec.build` "
             "(or __graft_entry__.build()) first")
     L = ctypes.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():

@@ -1,9 +1,9 @@
 """Build libtilec_hip.so in-tree with hipcc for gfx950.
 
-    python -m tilec_amd.build            # compile + link (always rebuilds)
+    python -m tilec.build            # compile + link (always rebuilds)
 
 Each .hip file under csrc/ is compiled to an object in csrc/_build/ in
-parallel, then linked into tilec_amd/libtilec_hip.so, which ext.py loads with
+parallel, then linked into tilec/libtilec_hip.so, which ext.py loads with
 ctypes.  The library is written for MI355X only (--offload-arch=gfx950).
 """
 

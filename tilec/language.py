@@ -1,5 +1,14 @@
-"""`tilec.language` host helpers (tilec/language.py), served by tilec_amd.language."""
+"""Host-side helpers of the reference's tile language that the matmul path uses.
 
-from tilec_amd.language import cdiv  # noqa: F401
+Only `cdiv` is on the hot path (grid math); the DSL builtins
+(`tl.load`, `tl.dot`, ...; tilec/language.py:1-14) belong to the tile compiler,
+which this implementation replaces with hand-written gfx950 kernels.
+"""
 
-__all__ = ["cdiv"]
+
+def cdiv(a, b):
+    """Ceiling division, for host code: cdiv(5000, 4096) == 2.
+
+    Restates tilec/language.py:16-18.
+    """
+    return (a + b - 1) // b
