@@ -104,7 +104,10 @@ int tilec_matmul(const void* x1, const void* x2, float* out,
 
 /*
  * Bytes of scratch (`workspace`) tilec_matmul needs for these arguments
- * (0 if none; the same for every layout).  Replaces nothing in the
+ * with both operands row-major and contiguous (0 if none).  For a named
+ * variant the size is the same for every layout; TILEC_VARIANT_AUTO may pick
+ * another variant for another layout or stride, which
+ * tilec_matmul_scratch_bytes accounts for.  Replaces nothing in the
  * reference (its kernel needs no scratch); the caller allocates it the way
  * `_matrix_mul_tiled` allocates `out` (tilec/ext.py:61).
  */
@@ -118,6 +121,20 @@ size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K,
                                   int32_t split_k);
 
 /*
+ * Both scratch sizes for exactly the arguments tilec_matmul gets (layout
+ * bits and strides included; ldx1 / ldx2 <= 0: contiguous), so that
+ * TILEC_VARIANT_AUTO is resolved as the call will resolve it.  Returns
+ * TILEC_OK, or the status tilec_matmul would return for an argument it
+ * rejects (sizes are then 0).  Like the two queries above it replaces
+ * nothing in the reference; it cannot see pointers, so for the row-dot and
+ * row-tile variants it counts the scratch of their streaming fallback.
+ */
+int tilec_matmul_scratch_bytes(int64_t M, int64_t N, int64_t K,
+                               int64_t ldx1, int64_t ldx2, int32_t layout,
+                               int32_t dtype, int32_t variant, int32_t split_k,
+                               size_t* workspace_bytes, size_t* counter_bytes);
+
+/*
  * tilec_matmul without the caller's scratch: for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation).  No counterpart in the reference, whose
@@ -127,7 +144,7 @@ size_t tilec_matmul_counter_bytes(int64_t M, int64_t N, int64_t K,
  * A split K uses a static array of the library on the current device: at
  * most 16 MiB of partial sums and 1 MiB of counters (each GPU the library
  * runs on holds 17 MiB until the process ends).  A call that needs more
- * (tilec_matmul_workspace_bytes / _counter_bytes) fails with
+ * (tilec_matmul_scratch_bytes for the same arguments) fails with
  * TILEC_ERR_WORKSPACE before anything is enqueued; use tilec_matmul then.
  * The first call on a device looks the array up and enqueues a small kernel
  * that clears its counters.  Nothing is allocated.

@@ -368,6 +368,63 @@ def test_noalloc_rejects_oversized_scratch_before_launch():
     assert L.tilec_matmul_noalloc(None, None, None, 0, 8, 8, 8, 8, 8, 0, 0, -1, 0, None) == _lib.OK
 
 
+def test_panel_variants_check_their_own_split_geometry():
+    # The panel kernel takes at least K / KC splits (KC = 512 fp32 / 256 bf16
+    # rows) and addresses its partials with 32-bit offsets: shapes whose
+    # partials reach 2 GiB, or whose splits pass the grid's 65535, are
+    # rejected before launch, and the size queries answer 0 for them.
+    L = _lib.lib()
+    pb = _lib.variant_id("skinny_bf16_p_v1_w8")
+    pf = _lib.variant_id("skinny_f32_p_v1_w8")
+    for v, dt, K in [(pb, _lib.BF16, 1 << 22), (pf, _lib.F32, 1 << 22)]:
+        assert L.tilec_matmul_workspace_bytes(1, 4096, K, dt, v, 0) == 0, (v, K)
+        assert _call(M=1, N=4096, K=K, dtype=dt, variant=v, split=0, ws=16, ws_bytes=1 << 40,
+                     cnt=16, cnt_bytes=1 << 30) == _lib.ERR_UNSUPPORTED
+        assert "2 GiB" in _lib.last_error()
+    assert _call(M=1, N=64, K=1 << 24, dtype=_lib.BF16, variant=pb, split=0) == _lib.ERR_VALUE
+    assert "65535" in _lib.last_error()
+    # the config-1 size still resolves: 8 splits x 32 panels of 16-row x 128-column partial slots
+    assert L.tilec_matmul_workspace_bytes(1, 4096, 4096, _lib.F32, pf, 8) == 8 * 32 * 16 * 128 * 4
+
+
+def _scratch(M, N, K, ldx1, ldx2, layout, dtype=0, variant=-1, split=0):
+    ws, cnt = ctypes.c_size_t(7), ctypes.c_size_t(7)
+    rc = _lib.lib().tilec_matmul_scratch_bytes(M, N, K, ldx1, ldx2, layout, dtype, variant, split,
+                                               ctypes.byref(ws), ctypes.byref(cnt))
+    return rc, ws.value, cnt.value
+
+
+def test_scratch_query_follows_layout_and_strides():
+    L = _lib.lib()
+    # M=8, K=200, N=64 with a row stride of x2 past the streaming kernel's
+    # 2^25 bound: the automatic pick is the direct kernel, whose split K
+    # needs scratch; the layout-blind query (contiguous strides) sees the
+    # streaming kernel instead.
+    ld = (1 << 25) + 64
+    rc, ws, cnt = _scratch(8, 64, 200, 0, ld, 0)
+    assert rc == _lib.OK and ws > 0 and cnt > 0
+    assert _lib.variants()[L.tilec_select_variant_layout(8, 64, 200, 0, 0, 0, ld)]["name"].startswith("direct_")
+    # the same answer as the layout-blind queries for contiguous row-major operands
+    for M, N, K in [(1, 4096, 4096), (16, 4096, 4096), (200, 3000, 1500), (4096, 4096, 4096)]:
+        assert _scratch(M, N, K, 0, 0, 0)[1:] == (L.tilec_matmul_workspace_bytes(M, N, K, 0, -1, 0),
+                                                   L.tilec_matmul_counter_bytes(M, N, K, 0, -1, 0))
+    # errors come back as tilec_matmul's status, with zero sizes
+    assert _scratch(-1, 8, 8, 0, 0, 0) == (_lib.ERR_VALUE, 0, 0)
+    assert _scratch(8, 8, 8, 0, 0, 4) == (_lib.ERR_VALUE, 0, 0)
+    assert _scratch(8, 8, 8, 0, 0, 0, dtype=5) == (_lib.ERR_TYPE, 0, 0)
+    assert _scratch(0, 8, 8, 0, 0, 0) == (_lib.OK, 0, 0)
+    # ext sizes a call with the same query
+    assert ext._scratch_sizes(8, 64, 200, 200, ld, 0, 0, -1, 0) == (ws, cnt)
+
+
+def test_hip_configs_of_empty_outputs():
+    for M, K, N in [(0, 64, 64), (4, 64, 0), (0, 0, 0)]:
+        for dt in ("f32", "bf16"):
+            cfgs = ext.hip_configs(M, K, N, dt)
+            assert isinstance(cfgs, list)
+            assert not any(c[0].startswith("direct_") for c in cfgs)
+
+
 def test_abi_empty_outputs_enqueue_nothing():
     # M == 0 or N == 0: nothing to do, no device access (null pointers are fine).
     assert _call(M=0, x1=None, x2=None, out=None) == _lib.OK

@@ -30,6 +30,8 @@ SIGNATURES = {
                                             _i32, _i32, _i32, _vp]),
     "tilec_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
     "tilec_matmul_counter_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
+    "tilec_matmul_scratch_bytes": (ctypes.c_int, [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
+                                                  ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "tilec_sum": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp]),
     "tilec_sum_workspace_bytes": (_sz, [_i64, _i64, _i32, _i32, _i32]),
     "tilec_sum_counter_bytes": (_sz, [_i64, _i64, _i32, _i32, _i32]),

@@ -58,6 +58,9 @@ struct VariantDesc {
   // row-tile kernels): true when a call runs the variant's own kernel.  The
   // size queries cannot see pointers, so they stay conservative.
   bool (*own_kernel_runs)(const MatmulArgs&) = nullptr;
+  // Split count a variant's own kernel runs for a requested split (nullptr:
+  // the family's own rule); checked against the grid's 65535 limit.
+  int64_t (*effective_splits)(const VariantDesc& d, int64_t N, int64_t K, int split_k) = nullptr;
 };
 
 // Workspace of a prep variant: a transposed copy of x1 (M x K) and of x2

@@ -327,6 +327,10 @@ size_t skinny_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int sp
 // wave and batch).
 static int panel_batch_rows(const VariantDesc& d) { return 2 * d.waves * d.unroll; }
 
+int64_t panel_effective_splits(const VariantDesc& d, int64_t N, int64_t K, int split_k) {
+  return panel_geom(N, K, split_k, d.bn, d.bk, panel_batch_rows(d)).splits;
+}
+
 size_t panel_workspace_bytes(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
   const PanelGeom g = panel_geom(N, K, split_k, d.bn, d.bk, panel_batch_rows(d));
   const size_t own = g.splits > 1 ? (size_t)g.splits * g.panels * kRows * d.bn * sizeof(float) : 0;
@@ -350,6 +354,7 @@ static VariantDesc panel_desc(const char* name, int dtype, int waves, int max_m,
                 kc, waves, max_m, bt, launch};
   d.workspace_bytes = panel_workspace_bytes;
   d.counter_bytes = panel_counter_bytes;
+  d.effective_splits = panel_effective_splits;
   d.wgs_per_cu = 1;
   return d;
 }

@@ -315,6 +315,16 @@ int resolve(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant, int
       const int rc = skinny_partials_check(d, M, N, K, s);
       if (rc != TILEC_OK) return rc;
     }
+    // Variants with their own split geometry (the panel kernel: at least
+    // K / KC splits, partials addressed with 32-bit offsets).  Their size
+    // query covers both their own kernel and the streaming fallback.
+    if (d->effective_splits && d->effective_splits(*d, N, K, s) > 65535)
+      return fail(TILEC_ERR_VALUE, "tilec: %s: K=%lld with split_k=%d gives more than 65535 splits", d->name,
+                  (long long)K, s);
+    if (d->workspace_bytes && M > 0 && N > 0 &&
+        (int64_t)d->workspace_bytes(*d, M, N, K, s) >= (int64_t(1) << 31))
+      return fail(TILEC_ERR_UNSUPPORTED, "tilec: %s: K=%lld needs 2 GiB or more of split-K partials", d->name,
+                  (long long)K);
   }
   *out_d = d;
   *out_split = s;
@@ -523,8 +533,9 @@ int tilec_matmul_noalloc(const void* x1, const void* x2, float* out, int64_t M, 
                          int64_t ldx1, int64_t ldx2, int64_t ldo, int32_t layout, int32_t dtype, int32_t variant,
                          int32_t split_k, void* stream) {
   g_err[0] = 0;
-  const size_t ws = tilec_matmul_workspace_bytes(M, N, K, dtype, variant, split_k);
-  const size_t cnt = tilec_matmul_counter_bytes(M, N, K, dtype, variant, split_k);
+  size_t ws = 0, cnt = 0;
+  const int qrc = tilec_matmul_scratch_bytes(M, N, K, ldx1, ldx2, layout, dtype, variant, split_k, &ws, &cnt);
+  if (qrc != TILEC_OK) return qrc;
   if (ws > kNoallocWsMax || cnt > kNoallocCntMax)
     return fail(TILEC_ERR_WORKSPACE,
                 "tilec: this call needs %zu bytes of scratch and %zu of counters; tilec_matmul_noalloc has %zu and "
@@ -538,6 +549,22 @@ int tilec_matmul_noalloc(const void* x1, const void* x2, float* out, int64_t M, 
   return tilec_matmul(x1, x2, out, M, N, K, ldx1, ldx2, ldo, layout, dtype, variant, split_k,
                       base, base ? kNoallocWsMax : 0, base ? base + kNoallocWsMax : nullptr,
                       base ? kNoallocCntMax : 0, stream);
+}
+
+int tilec_matmul_scratch_bytes(int64_t M, int64_t N, int64_t K, int64_t ldx1, int64_t ldx2, int32_t layout,
+                               int32_t dtype, int32_t variant, int32_t split_k, size_t* workspace_bytes,
+                               size_t* counter_bytes) {
+  g_err[0] = 0;
+  if (workspace_bytes) *workspace_bytes = 0;
+  if (counter_bytes) *counter_bytes = 0;
+  const VariantDesc* d = nullptr;
+  int s = 1;
+  const int rc = resolve(M, N, K, dtype, variant, split_k, &d, &s, ldx1, ldx2, layout);
+  if (rc != TILEC_OK) return rc;
+  if (M == 0 || N == 0) return TILEC_OK;
+  if (workspace_bytes) *workspace_bytes = variant_workspace_bytes(d, dtype, M, N, K, s);
+  if (counter_bytes) *counter_bytes = variant_counter_bytes(d, dtype, M, N, K, s);
+  return TILEC_OK;
 }
 
 size_t tilec_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t dtype, int32_t variant,

@@ -17,6 +17,7 @@ present.  The legacy config-space helpers of the reference (`plan`,
 `mm_configs`, ...) are kept with their original meaning.
 """
 
+import ctypes
 import re
 from functools import lru_cache
 
@@ -115,6 +116,8 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             # offered beside the powers of two; none whose partials would
             # reach the library's 2 GiB limit.
             tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
+            if tiles == 0:
+                continue  # an empty output: nothing for a K split to fill
             fills = [f for f in (device_cus() // tiles, 2 * device_cus() // tiles) if f > 1]
             seen = set()
             for s in sorted(set(_SKINNY_SPLITS) | set(fills)):
@@ -340,12 +343,17 @@ def _prepare(x1, x2):
 
 
 @lru_cache(4096)
-def _scratch_sizes(M, N, K, dtype, variant, split_k):
-    """(workspace, counter) bytes a call needs; the C ABI's answer depends
-    only on these arguments, so repeat calls skip two library crossings."""
-    L = _lib.lib()
-    return (L.tilec_matmul_workspace_bytes(M, N, K, dtype, variant, split_k),
-            L.tilec_matmul_counter_bytes(M, N, K, dtype, variant, split_k))
+def _scratch_sizes(M, N, K, lda, ldb, layout, dtype, variant, split_k):
+    """(workspace, counter) bytes a call needs, for exactly the arguments
+    tilec_matmul gets (layout and strides decide what TILEC_VARIANT_AUTO
+    runs); the C ABI's answer depends only on these arguments, so repeat
+    calls skip the library crossing."""
+    ws, cnt = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    rc = _lib.lib().tilec_matmul_scratch_bytes(M, N, K, lda, ldb, layout, dtype, variant, split_k,
+                                               ctypes.byref(ws), ctypes.byref(cnt))
+    if rc:
+        _lib.check(rc)
+    return ws.value, cnt.value
 
 
 def _launch(x1, x2, M, K, N, variant, split_k, ops=None):
@@ -360,7 +368,7 @@ def _launch(x1, x2, M, K, N, variant, split_k, ops=None):
         return out
     stream = torch.cuda.current_stream(x1.device).cuda_stream
     ws_ptr, ws_bytes, cnt_ptr, cnt_bytes = None, 0, None, 0
-    need, need_cnt = _scratch_sizes(M, N, K, dtype, variant, split_k)
+    need, need_cnt = _scratch_sizes(M, N, K, lda, ldb, layout, dtype, variant, split_k)
     if need:
         ws = workspace_for(x1.device, stream, need)
         ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
