@@ -14,7 +14,8 @@ and W warmup steps.  Extra objects in the same line:
                  M in {1,4,16} fp32 and {1,16} bf16, K=N=4096, x2 rotated
                  over 512 MiB of copies (beyond the 256 MB Infinity Cache),
                  launches replayed from a HIP graph so the host does not
-                 bound an 8 us kernel
+                 bound an 8 us kernel; with `floor`, one bare pass over the
+                 same x2 (tilec_read_floor), the fastest any GEMV can read it
   bf16_8192    — config 4, bf16 8192^3 with fp32 accumulate, vs 2.5 PFLOP/s
   configs      — every fp32 config (0, 2 at 1024/2048/4096, the 4 ragged
                  shapes of 3): device time per call from graph replay
@@ -69,7 +70,7 @@ def parse():
                    help="with --only skinny, configs or reduce: run only the cases whose key contains this "
                         "text (one kernel per profile run)")
     p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "vendor", "copy",
-                                      "host", "tuner", "cpu", "ksweep"],
+                                      "host", "tuner", "cpu", "ksweep", "floor"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -211,8 +212,47 @@ def _gemv_cases(ms_by_dtype, transposed, steps):
 
 def bench_skinny(steps=200):
     """M in {1,4,16} fp32 and {1,16} bf16 at K=N=4096: HBM GB/s from
-    graph-replayed launches over rotating x2 copies."""
-    return _gemv_cases((("f32", (1, 4, 16)), ("bf16", (1, 16))), False, steps)
+    graph-replayed launches over rotating x2 copies; beside them the read
+    floor of the same x2 (bench_floor)."""
+    out = _gemv_cases((("f32", (1, 4, 16)), ("bf16", (1, 16))), False, steps)
+    if CASE is None or CASE.startswith("floor"):
+        out["floor"] = bench_floor(steps)
+    return out
+
+
+def bench_floor(steps=200):
+    """The HBM read floor of the config-1 GEMV: one pass over a 4096 x 4096
+    x2 (64 MiB fp32, 32 MiB bf16) through tilec_read_floor — the moving
+    window of 16 KiB pieces the GEMV kernels' K splits imitate, two
+    workgroups per CU, non-temporal 16-byte loads, no cross-workgroup
+    combine — graph-replayed over rotating copies (>= 512 MiB) exactly as the
+    GEMV cases are.  A GEMV cannot read x2 faster than this."""
+    import ctypes
+    import torch
+    from tilec import _lib
+    L = _lib.lib()
+    out = {}
+    sink = torch.empty(1 << 18, dtype=torch.float32, device="cuda")
+    for dtype, esz in (("f32", 4), ("bf16", 2)):
+        nbytes = esz * 4096 * 4096
+        nbuf = (512 << 20) // nbytes
+        xs = [torch.full((nbytes // 4,), 1.0 + i, dtype=torch.float32, device="cuda") for i in range(nbuf)]
+
+        def read(x, _n=nbytes):
+            rc = L.tilec_read_floor(ctypes.c_void_p(x.data_ptr()), _n, ctypes.c_void_p(sink.data_ptr()), 0,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if rc:
+                _lib.check(rc)
+            return sink
+
+        us = _gemv(None, xs, steps, mm=lambda _x1, x: read(x), settle_ms=SETTLE_MS / 2)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[f"x2_{dtype}"] = dict(us=us, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, workgroups=min(
+            2 * torch.cuda.get_device_properties(0).multi_processor_count, nbytes // 16384))
+        log(f"read floor {dtype} x2 ({nbytes >> 20} MiB): {us:.2f} us/launch, {gbs:.0f} GB/s")
+        del xs
+    torch.cuda.synchronize()
+    return out
 
 
 def bench_layouts(steps=200, gemm_steps=20):
@@ -243,7 +283,12 @@ def bench_layouts(steps=200, gemm_steps=20):
     return out
 
 
-def bench_bf16(steps=20, warmup=2):
+def bench_bf16(steps=20, warmup=2, rounds=3):
+    """BASELINE config 4 (bf16 8192^3, fp32 accumulate and out), timed in
+    `rounds` interleaved rounds of this library and of torch.mm (hipBLASLt,
+    fp32 result) on the same inputs, each after its own clock settling; the
+    medians are reported, so the spread of one box does not decide the
+    comparison (the part is power-bound here and its clock moves with it)."""
     import torch
     from oracle import oracle as O
     from tilec import ext
@@ -252,10 +297,17 @@ def bench_bf16(steps=20, warmup=2):
     a = torch.from_numpy(O.normal((n, n), 8, std=sigma)).to(torch.bfloat16).cuda()
     b = torch.from_numpy(O.normal((n, n), 9, std=sigma)).to(torch.bfloat16).cuda()
     cfg = kernel_name_for(n, n, n, "bf16")
-    ms = timed(lambda: ext.matrix_mul(a, b), steps, warmup, settle_ms=SETTLE_MS)
-    tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
-    log(f"bf16 8192^3: {ms:.3f} ms, {tflops:.1f} TFLOP/s ({cfg})")
-    return dict(ms=ms, TFLOPs=tflops, frac=tflops / PEAK_BF16_MFMA, config=list(cfg))
+    mine, vend = [], []
+    for _ in range(rounds):
+        mine.append(timed(lambda: ext.matrix_mul(a, b), steps, warmup, settle_ms=SETTLE_MS))
+        vend.append(timed(lambda: _vendor_mm(a, b), steps, warmup, settle_ms=SETTLE_MS))
+    ms, vms = sorted(mine)[rounds // 2], sorted(vend)[rounds // 2]
+    tflops, vtflops = 2 * n ** 3 / (ms * 1e-3) / 1e12, 2 * n ** 3 / (vms * 1e-3) / 1e12
+    log(f"bf16 8192^3: {ms:.3f} ms, {tflops:.1f} TFLOP/s ({cfg}); torch.mm {vms:.3f} ms, {vtflops:.1f} TFLOP/s "
+        f"(medians of {rounds} interleaved rounds: {[round(x, 3) for x in mine]} / {[round(x, 3) for x in vend]})")
+    return dict(ms=ms, TFLOPs=tflops, frac=tflops / PEAK_BF16_MFMA, config=list(cfg), rounds=rounds,
+                ms_rounds=mine, torch_mm_ms=vms, torch_mm_TFLOPs=vtflops, torch_mm_ms_rounds=vend,
+                speedup_vs_torch_mm=vms / ms)
 
 
 def _vendor_mm(a, b):
@@ -689,7 +741,7 @@ def main():
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
                "configs": bench_configs, "layouts": bench_layouts, "reduce": bench_reduce,
                "vendor": bench_vendor, "copy": bench_copy, "host": bench_host, "tuner": bench_tuner,
-               "ksweep": bench_ksweep,
+               "ksweep": bench_ksweep, "floor": bench_floor,
                "cpu": lambda: bench_cpu(args.cpu_seconds)}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return

@@ -221,6 +221,19 @@ size_t tilec_sum_workspace_bytes(int64_t R, int64_t C, int32_t layout,
 size_t tilec_sum_counter_bytes(int64_t R, int64_t C, int32_t layout,
                                int32_t dtype, int32_t axis);
 
+/*
+ * The HBM read floor, a measurement aid with no counterpart in the
+ * reference: one pass over `bytes` of x (a multiple of 16 KiB, 16-byte
+ * aligned), in the order the GEMV kernels are measured against —
+ * `workgroups` workgroups (<= 0: two per CU; at most one per 16 KiB piece)
+ * read the 16 KiB pieces g, g + G, g + 2G, ... with non-temporal 16-byte
+ * loads (four waves per workgroup), so the chip reads one moving window.
+ * Wave w of workgroup g writes the fp32 sum of the floats it read to
+ * sink[4 g + w] (the caller provides four floats per workgroup); nothing is
+ * combined across workgroups.  Asynchronous on `stream`, allocates nothing.
+ */
+int tilec_read_floor(const void* x, size_t bytes, float* sink, int32_t workgroups, void* stream);
+
 /* Message describing the last failure on this thread ("" if none). */
 const char* tilec_last_error(void);
 

@@ -425,6 +425,17 @@ def test_hip_configs_of_empty_outputs():
             assert not any(c[0].startswith("direct_") for c in cfgs)
 
 
+def test_read_floor_rejects_bad_arguments_before_launch():
+    L = _lib.lib()
+    assert L.tilec_read_floor(16, 16384 + 16, 16, 0, None) == _lib.ERR_VALUE
+    assert "16 KiB" in _lib.last_error()
+    assert L.tilec_read_floor(8, 16384, 16, 0, None) == _lib.ERR_VALUE  # not 16-byte aligned
+    assert L.tilec_read_floor(None, 16384, 16, 0, None) == _lib.ERR_VALUE
+    assert L.tilec_read_floor(16, 16384, None, 0, None) == _lib.ERR_VALUE
+    assert L.tilec_read_floor(16, 16384, 16, -1, None) == _lib.ERR_VALUE
+    assert L.tilec_read_floor(None, 0, None, 0, None) == _lib.OK  # nothing to read
+
+
 def test_abi_empty_outputs_enqueue_nothing():
     # M == 0 or N == 0: nothing to do, no device access (null pointers are fine).
     assert _call(M=0, x1=None, x2=None, out=None) == _lib.OK

@@ -226,6 +226,43 @@ def test_mm_configs_characterisation():
         assert len(got) == len(O.mm_configs(M1, N, M2))  # no duplicates
 
 
+# Hand-derived known answers for the legacy config space (tilec/ext.py:29-51):
+# blocks(n) keeps the BLOCKS below plan(n)'s block that cut n into at most 16
+# chunks, then that block; mm_configs crosses the splits p with N // p >= 32,
+# the joins r <= M1 and the blocks of cdiv(N, p).
+BLOCKS_KNOWN = {
+    1: [1],                      # plan(1) = (1, 1)
+    31: [64],                    # plan(31): 64; no BLOCKS entry below 64
+    300: [256, 1024],            # plan(300): 1024; 256 cuts 300 into 2
+    4096: [256, 1024, 4096],     # 256 cuts 4096 into exactly 16
+    5000: [1024, 4096],          # 256 would take 20 chunks; 1024 takes 5
+    8192: [1024, 4096],          # block capped at 4096; 256 would take 32 chunks
+}
+MM_CONFIGS_KNOWN = {
+    (1, 31, 1): [(1, 1, 64)],    # 31 // 2 < 32: no split; M1 = 1: no join
+    (8, 48, 3): [(1, 1, 64), (1, 2, 64), (1, 4, 64), (1, 8, 64)],
+}
+MM_CONFIGS_COUNT = {
+    (129, 256, 32): 16,          # p in 1, 2, 4, 8 (256 // 16 < 32) x 4 joins x one block each
+    (4, 4096, 64): 39,           # 7 splits with 3 + 3 + 2 + 2 + 1 + 1 + 1 blocks, x joins 1, 2, 4
+}
+
+
+@pytest.mark.parametrize("impl", ["oracle", "ext"])
+def test_blocks_and_mm_configs_known_answers(impl):
+    from tilec import ext
+    blocks = O.blocks if impl == "oracle" else ext._blocks
+    mm_configs = O.mm_configs if impl == "oracle" else ext.mm_configs
+    for n, want in BLOCKS_KNOWN.items():
+        assert blocks(n) == want, n
+    for args, want in MM_CONFIGS_KNOWN.items():
+        assert mm_configs(*args) == want, args
+    for args, count in MM_CONFIGS_COUNT.items():
+        assert len(mm_configs(*args)) == count, args
+    # (4, 4096, 64): the largest split keeps one 64-element block
+    assert (64, 4, 64) in mm_configs(4, 4096, 64) and (64, 8, 64) not in mm_configs(4, 4096, 64)
+
+
 # ---------------------------------------------------------------------------
 # Sums (tl.sum, kernel1.py:8-15)
 # ---------------------------------------------------------------------------

@@ -148,3 +148,30 @@ def test_sum_full_size_properties():
     r, c = ext.sum(t, 1).double().sum(), ext.sum(t, 0).double().sum()
     assert abs(float(r - c)) <= 1e-5 * float(t.float().abs().sum())
     say("full-size properties ok")
+
+
+@pytest.mark.parametrize("pieces,workgroups", [(1, 0), (7, 3), (64, 0), (4096, 0), (4096, 1000)])
+def test_read_floor_sums(pieces, workgroups):
+    """tilec_read_floor (the HBM read floor the GEMV kernels are measured
+    against) reads every byte once: the four per-wave sums of workgroup g
+    over small-integer data add up to the exact sum of its own pieces
+    g, g + G, ..., and wave w's sum to that of 16-byte groups w, w + 4 of
+    each 1 KiB row of those pieces."""
+    import ctypes
+    n = pieces * 4096
+    x = O.small_ints((n,), 77 + pieces, -8, 8)
+    xd = dev(x)
+    L = _lib.lib()
+    G = min(workgroups or 2 * torch.cuda.get_device_properties(0).multi_processor_count, pieces)
+    sink = torch.full((4 * G + 1,), float("nan"), dtype=torch.float32, device="cuda")
+    say(f"read floor: {pieces} pieces, {G} workgroups")
+    _lib.check(L.tilec_read_floor(ctypes.c_void_p(xd.data_ptr()), 4 * n, ctypes.c_void_p(sink.data_ptr()),
+                                  workgroups, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    got = sink.cpu().numpy()
+    assert np.isnan(got[4 * G]), "wrote past its workgroups"
+    # a piece is 4 loads x 256 threads x 4 floats; thread t (wave t // 64)
+    # reads floats 4 (t + 256 u) .. + 3, u < 4
+    per = x.reshape(pieces, 4, 4, 64, 4).astype(np.int64).sum(axis=(1, 3, 4))  # [piece, wave]
+    want = np.array([[per[g::G, w].sum() for w in range(4)] for g in range(G)], dtype=np.float32).ravel()
+    np.testing.assert_array_equal(got[:4 * G], want)

@@ -34,6 +34,7 @@ SIGNATURES = {
                                                   ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "tilec_sum": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp]),
     "tilec_sum_workspace_bytes": (_sz, [_i64, _i64, _i32, _i32, _i32]),
+    "tilec_read_floor": (ctypes.c_int, [_vp, _sz, _vp, _i32, _vp]),
     "tilec_sum_counter_bytes": (_sz, [_i64, _i64, _i32, _i32, _i32]),
     "tilec_select_variant": (_i32, [_i64, _i64, _i64, _i32]),
     "tilec_select_variant_layout": (_i32, [_i64, _i64, _i64, _i32, _i32, _i64, _i64]),

@@ -339,7 +339,40 @@ hipError_t launch_reduce_t(const void* x, float* out, int64_t R, int64_t C, int6
   return hipGetLastError();
 }
 
+// The HBM read floor (a measurement aid): workgroup g of G reads the 16 KiB
+// pieces g, g + G, g + 2G, ... of x, each lane four 16-byte non-temporal
+// loads per piece, so the workgroups in flight read one moving window of
+// G pieces; wave w of workgroup g writes the sum of what it read to
+// sink[4 g + w] (no barrier, so no wave waits for another).  Nothing is
+// combined across workgroups: the time is that of one pass over x plus the
+// end of a kernel that stores something.
+__global__ __launch_bounds__(kNT) void read_floor_kernel(const unsigned char* __restrict__ x, int64_t pieces,
+                                                          float* __restrict__ sink) {
+  constexpr uint32_t kPiece = 16384;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t p = blockIdx.x; p < pieces; p += gridDim.x) {
+    const BufRsrc r = make_rsrc(x + p * kPiece, kPiece);
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(16u * (threadIdx.x + kNT * u)), 0,
+                                                                             kCpolNt));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc += v[u];
+  }
+  float t = (acc.x + acc.y) + (acc.z + acc.w);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
+  if ((threadIdx.x & 63) == 0) sink[kWaves * blockIdx.x + (threadIdx.x >> 6)] = t;
+}
+
 }  // namespace
+
+hipError_t launch_read_floor(const void* x, int64_t bytes, float* sink, int workgroups, hipStream_t stream) {
+  hipLaunchKernelGGL(read_floor_kernel, dim3((unsigned)workgroups), dim3(kNT), 0, stream,
+                     static_cast<const unsigned char*>(x), bytes / 16384, sink);
+  return hipGetLastError();
+}
 
 // x row-major R x C with row stride ld; the caller has checked the limits.
 hipError_t launch_reduce(const void* x, float* out, int64_t R, int64_t C, int64_t ld, int dtype, int axis,

@@ -35,6 +35,7 @@ size_t reduce_workspace_bytes(const ReduceGeom& g);
 size_t reduce_counter_bytes(const ReduceGeom& g);
 hipError_t launch_reduce(const void* x, float* out, int64_t R, int64_t C, int64_t ld, int dtype, int axis, float* ws,
                          unsigned* counters, hipStream_t stream);
+hipError_t launch_read_floor(const void* x, int64_t bytes, float* sink, int workgroups, hipStream_t stream);
 }  // namespace tilec
 
 using namespace tilec;
@@ -453,6 +454,25 @@ int tilec_sum(const void* x, float* out, int64_t R, int64_t C, int64_t ldx, int3
                                      static_cast<float*>(workspace), static_cast<unsigned*>(counters),
                                      static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(TILEC_ERR_HIP, "tilec: launching the sum failed: %s", hipGetErrorString(e));
+  return TILEC_OK;
+}
+
+int tilec_read_floor(const void* x, size_t bytes, float* sink, int32_t workgroups, void* stream) {
+  g_err[0] = 0;
+  constexpr size_t kPiece = 16384;
+  if (bytes % kPiece != 0)
+    return fail(TILEC_ERR_VALUE, "tilec: read floor: bytes=%zu is not a multiple of 16 KiB", bytes);
+  if (bytes > (size_t(1) << 40)) return fail(TILEC_ERR_VALUE, "tilec: read floor: bytes=%zu is too large", bytes);
+  if (workgroups < 0) return fail(TILEC_ERR_VALUE, "tilec: read floor: workgroups=%d < 0", workgroups);
+  if (bytes == 0) return TILEC_OK;
+  if (x == nullptr || sink == nullptr) return fail(TILEC_ERR_VALUE, "tilec: read floor: x/sink is NULL");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0)
+    return fail(TILEC_ERR_VALUE, "tilec: read floor: x is not 16-byte aligned");
+  const int64_t pieces = (int64_t)(bytes / kPiece);
+  int64_t g = workgroups > 0 ? workgroups : 2 * (int64_t)device_cus();
+  if (g > pieces) g = pieces;
+  const hipError_t e = launch_read_floor(x, (int64_t)bytes, sink, (int)g, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(TILEC_ERR_HIP, "tilec: launching the read floor failed: %s", hipGetErrorString(e));
   return TILEC_OK;
 }
 
