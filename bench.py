@@ -485,11 +485,6 @@ def bench_reduce(reps=8):
     return out
 
 
-# Shapes absent from the tuner's timing table (tilec/mm_bench_mi355x.csv),
-# one or more per regime: GEMV, small output, medium, large fp32 and bf16.
-TUNER_UNSEEN = [(5, 3000, 2500, "f32"), (12, 6000, 1000, "bf16"), (48, 2900, 1800, "f32"), (96, 4000, 640, "f32"),
-                (200, 1500, 3000, "f32"), (777, 777, 777, "f32"), (1500, 3100, 900, "f32"),
-                (2000, 3000, 1000, "bf16"), (3000, 2000, 5000, "bf16")]
 
 
 def bench_tuner():
@@ -503,7 +498,7 @@ def bench_tuner():
     model = tune._model()
     g = torch.Generator(device="cuda").manual_seed(0)
     cases = []
-    for M, K, N, dtype in TUNER_UNSEEN:
+    for M, K, N, dtype in tune.UNSEEN_SHAPES:
         if CASE is not None and CASE not in f"{M}x{K}x{N}_{dtype}":
             continue
         assert (M, K, N, dtype, 0) not in model.best, "an unseen shape is in the tuner's table"

@@ -184,24 +184,54 @@ def test_row_dot_configs_only_where_the_kernel_runs():
 
 def test_tune_features_and_shapes():
     f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8)
-    assert len(f) == 19 and all(math.isfinite(x) for x in f) and f[-3:-1] == [0.0, 0.0]
-    assert tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8, layout=3)[-3:-1] == [1.0, 1.0]
-    assert tune.features(1, 4096, 4096, 256, "f32", "skinny_f32_v1_w4_b2", 4)[-1] == 1.0
-    s = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6)
-    assert s == tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6)
+    assert len(f) == 28 and all(math.isfinite(x) for x in f) and f[16:18] == [0.0, 0.0]
+    assert tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8, layout=3)[16:18] == [1.0, 1.0]
+    assert tune.features(1, 4096, 4096, 256, "f32", "skinny_f32_v1_w4_b2", 4)[18] == 1.0
+    s = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6, n_medium=0, n_narrow=0)
+    assert s == tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6, n_medium=0, n_narrow=0)
     rm = [x for x in s if x[4] == 0]
     lay = [x for x in s if x[4] != 0]
     assert len(rm) == 120 + len(tune.CONFIG_SHAPES) and len(lay) == 40 + len(tune.LAYOUT_CONFIG_SHAPES) + 10 + 6
     # the x @ W.T streams (M <= 4 and 5 <= M <= 16, x2 column-major) add to, and do not change, the others
-    no_rows = tune.shapes(120, seed=0, n_layout=40, n_rows=0, n_tile=6)
+    no_rows = tune.shapes(120, seed=0, n_layout=40, n_rows=0, n_tile=6, n_medium=0, n_narrow=0)
     assert set(no_rows) <= set(s) and all(x[0] <= 4 and x[4] == 2 for x in set(s) - set(no_rows))
-    no_tile = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=0)
+    no_tile = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=0, n_medium=0, n_narrow=0)
     assert set(no_tile) <= set(s) and all(5 <= x[0] <= 16 and x[4] == 2 for x in set(s) - set(no_tile))
     assert {x + (0,) for x in tune.CONFIG_SHAPES} <= set(rm) and set(tune.LAYOUT_CONFIG_SHAPES) <= set(lay)
     assert {x[4] for x in lay} == {1, 2, 3}
     assert any(m <= 16 for m, *_ in s) and any(d == "bf16" for _, _, _, d, _ in s)
     # the row-major draws do not depend on the layout stream
-    assert rm == [x for x in tune.shapes(120, seed=0, n_layout=5) if x[4] == 0]
+    assert rm == [x for x in tune.shapes(120, seed=0, n_layout=5, n_medium=0, n_narrow=0) if x[4] == 0]
+    # the medium and narrow streams add row-major shapes in their ranges, and
+    # never a shape the tuner must leave unseen
+    full = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6)
+    more = set(full) - set(s)
+    assert set(s) <= set(full) and 100 <= len(more) <= 140 and all(x[4] == 0 for x in more)
+    for M, K, N, d, _ in more:
+        small, large = min(M, N), max(M, N)
+        assert (48 <= small <= 600 and 500 <= large <= 6000 and 500 <= K <= 4096) or \
+            (48 <= small <= 400 and 500 <= large <= 5000 and 2048 <= K <= 16384), (M, K, N)
+    assert {d for *_, d, _ in more} == {"f32", "bf16"}
+    assert not {u + (0,) for u in tune.UNSEEN_SHAPES} & set(tune.shapes(400))
+
+
+def test_tune_roofline_known_answers():
+    # 4096^3 fp32 on the 256x256 tile: 256 tiles, one round of one workgroup
+    # per CU, no padding; the matrix-peak time 2 * 4096^3 / 157.3e12 bounds it
+    t_est, t_c, t_m, t_r, pad, tail, fill, kpw, rounds = tune.roofline(
+        4096, 4096, 4096, 256, "f32", "gemm_f32_256x256x32_w2x4_lds", 1)
+    assert (pad, tail, fill, rounds) == (1.0, 1.0, 1.0, 1.0)
+    assert t_c == pytest.approx(2 * 4096 ** 3 / 157.3e12)
+    assert t_m == pytest.approx(3 * 4 * 4096 ** 2 / 8e12)
+    assert t_r == pytest.approx(4 * 2 * 4096 ** 2 * 16 / 20e12)
+    assert t_est == pytest.approx(t_c + 3e-6) and kpw == 4096 / 8
+    # 1 x 4096 @ 4096 x 4096 on the streaming kernel, split 8: 64 slabs of 16 x 64
+    # (1/16 of each used), 512 workgroups of 8 waves = 2 rounds; HBM-bound
+    t_est, t_c, t_m, t_r, pad, tail, fill, kpw, rounds = tune.roofline(
+        1, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8)
+    assert (pad, rounds, fill) == (1 / 16, 2.0, 1.0)
+    assert t_m == pytest.approx((4 * (4096 + 4096 ** 2) + 4 * 4096 + 8 * 64 * 16 * 64 * 8) / 8e12)
+    assert t_est == pytest.approx(max(t_c, t_m, t_r) + 3e-6 + 1.5e-6)
 
 
 def test_tune_rotating_operands():
