@@ -184,7 +184,11 @@ def test_row_dot_configs_only_where_the_kernel_runs():
 
 def test_tune_features_and_shapes():
     f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8)
-    assert len(f) == 28 and all(math.isfinite(x) for x in f) and f[16:18] == [0.0, 0.0]
+    assert len(f) == 30 and all(math.isfinite(x) for x in f) and f[16:18] == [0.0, 0.0] and f[28:] == [1.0, 1.0]
+    # alignment of each operand's contiguous extent: x1 row-major runs along K, x2 column-major along K
+    assert tune.features(5, 4097, 4096, 256, "f32", "skinny_f32_w8_b1", 1)[28:] == [0.0, 1.0]
+    assert tune.features(5, 4096, 4100, 256, "bf16", "skinny_bf16_w8_b1", 1)[28:] == [1.0, 0.0]
+    assert tune.features(6, 4096, 4100, 256, "bf16", "skinny_bf16_w8_b1", 1, layout=3)[28:] == [0.0, 1.0]
     assert tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8, layout=3)[16:18] == [1.0, 1.0]
     assert tune.features(1, 4096, 4096, 256, "f32", "skinny_f32_v1_w4_b2", 4)[18] == 1.0
     s = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6, n_medium=0, n_narrow=0)

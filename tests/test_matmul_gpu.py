@@ -238,7 +238,7 @@ def test_skinny_fma_path():
 
 
 def panel_variants():
-    return [v for v in _lib.variants() if "_p_" in v["name"]]
+    return [v for v in _lib.variants() if ext.panel_variant(v)]
 
 
 def test_panel_kernel():

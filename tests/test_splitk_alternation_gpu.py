@@ -46,6 +46,7 @@ MATMUL_CASES = [
     ("streaming", ("skinny_f32_w8_b1", 8), (16, 4096, 1024), torch.float32),
     ("panel", ("skinny_f32_p_v1_w8", 8), (1, 4096, 4096), torch.float32),
     ("panel bf16", ("skinny_bf16_p_v1_w8", 16), (1, 4096, 4096), torch.bfloat16),
+    ("panel, M <= 4", ("skinny_f32_p_v4_w8", 8), (3, 4096, 4096), torch.float32),
     ("direct", ("direct_f32_32x64_w4_db", 8), (127, 1000, 513), torch.float32),
     ("tile GEMM", ("gemm_f32_64x64x16_w2x2", 8), (100, 4096, 200), torch.float32),
     ("streaming bf16", ("skinny_bf16_w8_b1", 8), (16, 4096, 1024), torch.bfloat16),

@@ -108,6 +108,10 @@ __device__ __forceinline__ f32x4 mfma16x16x32bf16(bf16x8 a, bf16x8 b, f32x4 c) {
 // ---------------------------------------------------------------------------
 typedef __amdgpu_buffer_rsrc_t BufRsrc;
 constexpr uint32_t kOob = 0x80000000u;
+// kOob when !ok, else 0: or-ed into an offset below 2^31 it masks the access
+// with no select (a select around the offset's arithmetic can become a
+// branch).
+__device__ __forceinline__ uint32_t oob_unless(bool ok) { return (uint32_t)!ok << 31; }
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
 
 __device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t num_records = 0x7FFFFFFFu) {

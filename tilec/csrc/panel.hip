@@ -152,47 +152,79 @@ __global__ __launch_bounds__(WAVES * 64) void panel_kernel(const T* __restrict__
     else return __int_as_float((int)__builtin_amdgcn_raw_buffer_load_b16(rx1, (int)o, 0, 0) << 16);
   };
 
+  // Rows past K are masked by the resources' extents: a batch's x2
+  // resource ends at its last row before K, and so does its x1 resource
+  // when M <= 1 and x1 is row-major (offsets stay below R rows: the launcher
+  // checks KC * ldx2 and KC * ldx1 fit in 31 bits).  Columns past N: the
+  // lane's base offset is kOob, and kOob plus an offset below 2^31 stays out
+  // of range.  No select or compare per load: around the offset arithmetic
+  // one became a branch per load.
+  constexpr bool kX1Extent = MV == 1 && !CA;
+  const uint32_t lane_off = gok ? EB * (uint32_t)(CPL * cq) : kOob;
+  // (Every input is wave-uniform; make_rsrc_uniform keeps the resources in
+  // scalar registers, which the min / max of the row count would otherwise
+  // lose, wrapping each load in a waterfall loop.)
+  auto x2_rsrc = [&](int64_t row0, int rows) {
+    return make_rsrc_uniform(x2 + row0 * ldx2 + n0, (uint32_t)max(rows, 0) * (uint32_t)ldx2 * EB);
+  };
+  auto x1_rsrc = [&](int64_t row0, int rows) {
+    return make_rsrc_uniform(CA ? x1 + row0 * ldx1 : x1 + row0, kX1Extent ? (uint32_t)max(rows, 0) * EB : 0x7FFFFFFFu);
+  };
+
   float acc[MV][CPL];
 #pragma unroll
   for (int m = 0; m < MV; ++m)
 #pragma unroll
     for (int c = 0; c < CPL; ++c) acc[m][c] = 0.f;
-  // Batches of BT row pairs per wave, fully unrolled up to KC / R; the
-  // workgroup stops after its last batch.  x1: every lane of a row needs
-  // the same MV values; for M == 1 each lane loads its own (one address per
-  // row), for M <= 4 lane cq < MV of the row loads x1[cq][row] and the row's
-  // lanes take them by shuffles.  Rows past K load zeros from both operands.
-#pragma unroll
-  for (int b0 = 0; b0 < PPW; b0 += BT) {
-    const int bi = b0 / BT;
-    if (bi >= nbat) break;  // workgroup-uniform
-    const int kb = (bi * S + split) * R;
-    const BufRsrc rx2 = make_rsrc(x2 + (int64_t)kb * ldx2 + n0);
-    const BufRsrc rx1 = make_rsrc(CA ? x1 + (int64_t)kb * ldx1 : x1 + kb);
-    const int left = K - kb;  // rows of K from the batch's first row
+  // Batches of BT row pairs per wave, fully unrolled up to KC / R.  x1:
+  // every lane of a row needs the same MV values; for M == 1 each lane loads
+  // its own (one address per row), for M <= 4 lane cq < MV of the row loads
+  // x1[cq][row] and the row's lanes take them by shuffles once it has
+  // arrived.  Rows past K load zeros from both operands.
+  struct Batch {
     V v[BT];
-    float a[BT][MV];
+    float x[BT];  // the lane's own x1 load
+  };
+  auto load_batch = [&](int bi, Batch& B) __attribute__((always_inline)) {
+    const int kb = (bi * S + split) * R;  // the batch's first row
+    const int left = K - kb;               // rows of K from it
+    const BufRsrc rx2 = x2_rsrc(kb, min(left, R));
+    const BufRsrc rx1 = x1_rsrc(kb, min(left, R));
 #pragma unroll
     for (int q = 0; q < BT; ++q) {
       const int row = 2 * (q * WAVES + wave) + rr;
-      const bool rok = row < left;
-      v[q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(
-                                       rx2, (int)((rok & gok) ? EB * ((uint32_t)row * (uint32_t)ldx2 + (uint32_t)(CPL * cq)) : kOob),
-                                       0, kCpolX2));
-      if constexpr (MV == 1) {
-        a[q][0] = ld_x1(rx1, (rok & (M > 0)) ? x1_off(0, row) : kOob);
-      } else {
-        const float mine = ld_x1(rx1, (rok & (cq < MV) & (cq < M)) ? x1_off(cq, row) : kOob);
-#pragma unroll
-        for (int m = 0; m < MV; ++m) a[q][m] = __shfl(mine, (lane & 32) + m);
-      }
+      B.v[q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rx2, (int)(lane_off + EB * (uint32_t)row * (uint32_t)ldx2), 0, kCpolX2));
+      // Explicit masks (x1 column-major or M > 1) get bit 31 or-ed in: every
+      // offset here is below 2^31 when the element is valid.
+      if constexpr (kX1Extent) B.x[q] = ld_x1(rx1, x1_off(0, row));
+      else if constexpr (MV == 1) B.x[q] = ld_x1(rx1, oob_unless((row < left) & (M > 0)) | x1_off(0, row));
+      else B.x[q] = ld_x1(rx1, oob_unless((row < left) & (cq < MV) & (cq < M)) | x1_off(cq, row));
     }
+  };
+  auto fma_batch = [&](const Batch& B) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < BT; ++q)
+    for (int q = 0; q < BT; ++q) {
+      float a[MV];
+      if constexpr (MV == 1) a[0] = B.x[q];
+      else {
+#pragma unroll
+        for (int m = 0; m < MV; ++m) a[m] = __shfl(B.x[q], (lane & 32) + m);
+      }
 #pragma unroll
       for (int m = 0; m < MV; ++m)
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[m][c] = __builtin_fmaf(a[q][m], elem<T>(v[q], c), acc[m][c]);
+        for (int c = 0; c < CPL; ++c) acc[m][c] = __builtin_fmaf(a[m], elem<T>(B.v[q], c), acc[m][c]);
+    }
+  };
+  // One batch at a time (the chip's workgroups then read one window of
+  // rows); the workgroup stops after its last batch.
+#pragma unroll
+  for (int bi = 0; bi < PPW / BT; ++bi) {
+    if (bi >= nbat) break;  // workgroup-uniform
+    Batch B;
+    load_batch(bi, B);
+    fma_batch(B);
   }
 
   // The two rows of a pair meet in a shuffle, the waves in LDS (wave order).
@@ -327,17 +359,21 @@ size_t skinny_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int sp
 // wave and batch).
 static int panel_batch_rows(const VariantDesc& d) { return 2 * d.waves * d.unroll; }
 
+static PanelGeom panel_geom_of(const VariantDesc& d, int64_t N, int64_t K, int split_k) {
+  return panel_geom(N, K, split_k, d.bn, d.bk, panel_batch_rows(d));
+}
+
 int64_t panel_effective_splits(const VariantDesc& d, int64_t N, int64_t K, int split_k) {
-  return panel_geom(N, K, split_k, d.bn, d.bk, panel_batch_rows(d)).splits;
+  return panel_geom_of(d, N, K, split_k).splits;
 }
 
 size_t panel_workspace_bytes(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
-  const PanelGeom g = panel_geom(N, K, split_k, d.bn, d.bk, panel_batch_rows(d));
+  const PanelGeom g = panel_geom_of(d, N, K, split_k);
   const size_t own = g.splits > 1 ? (size_t)g.splits * g.panels * kRows * d.bn * sizeof(float) : 0;
   return std::max(own, skinny_workspace_bytes(d.dtype, M, N, K, split_k));
 }
 size_t panel_counter_bytes(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
-  const PanelGeom g = panel_geom(N, K, split_k, d.bn, d.bk, panel_batch_rows(d));
+  const PanelGeom g = panel_geom_of(d, N, K, split_k);
   const size_t own = g.splits > 1 ? (size_t)g.panels * kCounterStride * sizeof(unsigned) : 0;
   return std::max(own, skinny_counter_bytes(d.dtype, M, N, K, split_k));
 }

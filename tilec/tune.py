@@ -93,7 +93,12 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
     decide occupancy: workgroups launched per CU and the K rows per split,
     the operand layout bits (x1, x2 column-major) and the variant's row
     bound (max_m; 0 = any M), which tells the FMA streaming variants apart;
-    then the analytic terms of `roofline` (times as log2 seconds).
+    then the analytic terms of `roofline` (times as log2 seconds), and
+    whether each operand's contiguous extent (K or M for x1, N or K for x2)
+    is a whole number of 16-byte groups: the direct-to-LDS, row-dot and
+    row-tile kernels take only such operands and run a slower fallback of
+    the same tile for the others, a difference the sizes alone do not show
+    the trees (on MI355X it took the held-out worst case from 2.3x to 1.5x).
     """
     v = _variant_by_name()[kernel]
     tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
@@ -107,7 +112,14 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
             lg(cdiv(K, split_k)), lg(M * K * N),
             float(layout & _lib.X1_COL_MAJOR != 0), float(layout & _lib.X2_COL_MAJOR != 0),
             float(v["max_m"]),
-            ls(t_est), ls(t_c), ls(t_m), ls(t_r), pad, tail, fill, lg(kpw), rounds]
+            ls(t_est), ls(t_c), ls(t_m), ls(t_r), pad, tail, fill, lg(kpw), rounds,
+            float(aligned(M if layout & _lib.X1_COL_MAJOR else K, dtype)),
+            float(aligned(K if layout & _lib.X2_COL_MAJOR else N, dtype))]
+
+
+def aligned(extent, dtype):
+    """A contiguous extent of whole 16-byte groups (4 fp32 / 8 bf16 elements)."""
+    return extent % (4 if dtype == "f32" else 8) == 0
 
 
 GRAPH_BELOW_MS = 0.2   # calls shorter than this are timed from a replayed HIP graph
