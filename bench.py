@@ -248,7 +248,8 @@ def bench_floor(steps=200):
         us = _gemv(None, xs, steps, mm=lambda _x1, x: read(x), settle_ms=SETTLE_MS / 2)
         gbs = nbytes / (us * 1e-6) / 1e9
         out[f"x2_{dtype}"] = dict(us=us, GBps=gbs, frac=gbs / PEAK_HBM, bytes=nbytes, workgroups=min(
-            2 * torch.cuda.get_device_properties(0).multi_processor_count, nbytes // 16384))
+            2 * torch.cuda.get_device_properties(0).multi_processor_count, nbytes // 16384),
+            traffic=traffic_of("read_floor", nbytes, 1, 1))
         log(f"read floor {dtype} x2 ({nbytes >> 20} MiB): {us:.2f} us/launch, {gbs:.0f} GB/s")
         del xs
     torch.cuda.synchronize()
