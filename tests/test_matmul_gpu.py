@@ -604,6 +604,34 @@ def test_bf16_variant_layouts(name):
                 assert O.rel_l2(got, ref) <= 1e-5, (name, layout, s, (m, k, n))
 
 
+# (M, K steps, N): K = steps x the variant's K step
+M16_STEP_SHAPES = [(300, 1, 260), (300, 3, 260), (257, 5, 513), (300, 6, 260), (520, 33, 264), (64, 10, 600)]
+
+
+@pytest.mark.parametrize("name", [v["name"] for v in _lib.variants() if "_m16" in v["name"]])
+def test_bf16_m16_step_counts(name):
+    """The 16x16x32 tile kernels with K a multiple of their K step: odd and
+    even step counts (a 32-deep step runs an odd count as the next even one,
+    the extra step on zeros) and the remainder after the unrolled ring, in
+    every layout: the fp64 oracle on bf16 inputs, and the exact integer
+    product on small integers."""
+    v = _lib.variants()[_lib.variant_id(name)]
+    for i, (m, steps, n) in enumerate(M16_STEP_SHAPES):
+        k = steps * v["bk"]
+        a16 = O.bf16_round(O.normal((m, k), 640 + 2 * i))
+        b16 = O.bf16_round(O.normal((k, n), 641 + 2 * i))
+        ref = O.matmul_bf16_f64(a16, b16)
+        ai = O.small_ints((m, k), 660 + 2 * i, -3, 3)
+        bi = O.small_ints((k, n), 661 + 2 * i, -3, 3)
+        want = (ai.astype(np.int64) @ bi.astype(np.int64)).astype(np.float32)
+        for layout in [0] + LAYOUTS:
+            say(f"{name} layout {layout} shape {(m, k, n)}")
+            got = run_layout(dev_bf16(a16), dev_bf16(b16), layout, (name, 1))
+            assert O.rel_l2(got, ref) <= 1e-5, (name, layout, (m, k, n))
+            got = run_layout(dev(ai, torch.bfloat16), dev(bi, torch.bfloat16), layout, (name, 1))
+            np.testing.assert_array_equal(got, want)
+
+
 def test_f32_lds_copies_strides_and_fallbacks():
     """The fp32 tiles with direct-to-LDS copies (*_lds) against the fp64
     oracle and, where the library has one, the register-staged variant of

@@ -305,6 +305,36 @@ __device__ __forceinline__ bool splitk_tile(f32x16 (&acc)[TM][TN], int split, in
   }
 }
 
+// splitk_tile for 16x16 MFMA blocks: lane l holds rows 4 (l / 16) .. +3 of
+// column l % 16 of each block as one float4 (row_base and col_base are the
+// lane's first row and column in block (0, 0)); live when the first of its
+// rows is below M and its column below N.
+template <int TM, int TN, int NT>
+__device__ __forceinline__ bool splitk_tile16(f32x4 (&acc)[TM][TN], int split, int S, int tile, int tiles,
+                                              float* __restrict__ ws, unsigned* __restrict__ counters,
+                                              int* last_flag, int row_base, int col_base, int M, int N) {
+  constexpr int NV = TM * TN;
+  if constexpr (NV * 4 > kSplitMaxAccPerThread) {
+    return true;  // never split (the host passes S == 1 for these tiles)
+  } else {
+  f32x4 v[NV];
+  bool live[NV];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      v[i * TN + j] = acc[i][j];
+      live[i * TN + j] = (row_base + 16 * i < M) & (col_base + 16 * j < N);
+    }
+  if (!splitk_combine<NT, NV>(v, live, split, S, tile, tiles, ws, counters, last_flag)) return false;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = v[i * TN + j];
+  return true;
+  }
+}
+
 // K splits of a tile kernel: `steps` K steps of BK per split (the last may
 // be shorter), `splits` = how many are non-empty.  K == 0: one empty split.
 struct SplitGeom {

@@ -230,7 +230,7 @@ hipError_t launch_one(const MatmulArgs& a, dim3 grid) {
 
 }  // namespace
 
-template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB>
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB, int MF>
 hipError_t launch_gemm_bf16_lds(const MatmulArgs& a);  // gemm_bf16_lds.hip
 
 namespace {
@@ -241,7 +241,7 @@ namespace {
 // above with the same output tile (NBUF == 0: generic kernel only).  Both
 // use the variant's WM x WN waves, so a K split is possible in one exactly
 // when it is in the other.
-template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB>
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, bool CA, bool CB, int MF>
 hipError_t launch_layout(const MatmulArgs& a) {
   const int64_t tiles = cdiv(a.M, BM) * cdiv(a.N, BN);
   if (tiles == 0) return hipSuccess;
@@ -257,7 +257,7 @@ hipError_t launch_layout(const MatmulArgs& a) {
     // BK rows for an r-contiguous one.
     const int64_t a_rows = CA ? BK : BM, b_rows = CB ? BN : BK;
     if (vec && a_rows * a.ldx1 * 2 < (int64_t(1) << 31) - 4096 && b_rows * a.ldx2 * 2 < (int64_t(1) << 31) - 4096)
-      return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, CA, CB>(a);
+      return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, CA, CB, MF>(a);
   }
   dim3 grid((unsigned)tiles);
   return vec ? launch_one<BM, BN, 64, WM, WN, true, CA, CB>(a, grid)
@@ -270,13 +270,13 @@ hipError_t launch_layout(const MatmulArgs& a) {
 // runs the generic kernel above with the same output tile (NBUF == 0: generic
 // kernel only).  Both use the variant's WM x WN waves, so a K split is
 // possible in one exactly when it is in the other.
-template <int BM, int BN, int BK, int NBUF, int WM = 2, int WN = 2>
+template <int BM, int BN, int BK, int NBUF, int WM = 2, int WN = 2, int MF = 32>
 hipError_t launch_gemm_bf16(const MatmulArgs& a) {
   switch (a.layout & 3) {
-    case 0: return launch_layout<BM, BN, BK, NBUF, WM, WN, false, false>(a);
-    case TILEC_X1_COL_MAJOR: return launch_layout<BM, BN, BK, NBUF, WM, WN, true, false>(a);
-    case TILEC_X2_COL_MAJOR: return launch_layout<BM, BN, BK, NBUF, WM, WN, false, true>(a);
-    default: return launch_layout<BM, BN, BK, NBUF, WM, WN, true, true>(a);
+    case 0: return launch_layout<BM, BN, BK, NBUF, WM, WN, false, false, MF>(a);
+    case TILEC_X1_COL_MAJOR: return launch_layout<BM, BN, BK, NBUF, WM, WN, true, false, MF>(a);
+    case TILEC_X2_COL_MAJOR: return launch_layout<BM, BN, BK, NBUF, WM, WN, false, true, MF>(a);
+    default: return launch_layout<BM, BN, BK, NBUF, WM, WN, true, true, MF>(a);
   }
 }
 
@@ -331,7 +331,7 @@ hipError_t transpose_bf16(const void* in, void* out, int64_t R, int64_t C, int64
 // walks each operand along its rows; on 8192^3 it runs about 18% faster than
 // row-major x2.  Shapes the aligned kernel cannot take, and operands already
 // k-contiguous, run the plain variant.
-template <int BM, int BN, int BK, int NBUF, int WM, int WN>
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, int MF = 32>
 hipError_t launch_gemm_bf16_kc(const MatmulArgs& a) {
   const bool ca = a.layout & TILEC_X1_COL_MAJOR, cb = a.layout & TILEC_X2_COL_MAJOR;
   auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -339,7 +339,7 @@ hipError_t launch_gemm_bf16_kc(const MatmulArgs& a) {
                   aligned(a.x1) && aligned(a.x2) && aligned(a.workspace) && a.K > 0 &&
                   (int64_t)BM * a.K * 2 < (int64_t(1) << 31) - 4096 && (int64_t)BN * a.K * 2 < (int64_t(1) << 31) - 4096 &&
                   a.M * a.K < (int64_t(1) << 31) && a.K * a.N < (int64_t(1) << 31);
-  if (!ok || (!ca && cb)) return launch_gemm_bf16<BM, BN, BK, NBUF, WM, WN>(a);
+  if (!ok || (!ca && cb)) return launch_gemm_bf16<BM, BN, BK, NBUF, WM, WN, MF>(a);
   MatmulArgs b = a;
   char* ws = static_cast<char*>(a.workspace);
   if (ca) {  // x1 is [K][M] in memory: its transpose is x1 row-major [M][K]
@@ -360,7 +360,7 @@ hipError_t launch_gemm_bf16_kc(const MatmulArgs& a) {
   b.workspace = nullptr;
   b.workspace_bytes = 0;
   b.counters = nullptr;
-  return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, false, true>(b);
+  return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, false, true, MF>(b);
 }
 
 }  // namespace
@@ -392,6 +392,19 @@ const VariantDesc* gemm_bf16_variants(int* count) {
        launch_gemm_bf16<256, 256, 32, 4, 2, 4>},
       {"gemm_bf16_256x256x32_r4w8_kc", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 32, 8, 0, 4,
        launch_gemm_bf16_kc<256, 256, 32, 4, 2, 4>, 1},
+      // 16x16x32 MFMAs (the same tiles; K % BK != 0 runs the 32x32 kernel)
+      {"gemm_bf16_256x256x64_r2_m16", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 64, 8, 0, 2,
+       launch_gemm_bf16<256, 256, 64, 2, 2, 4, 16>},
+      {"gemm_bf16_256x256x32_r4w8_m16", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 32, 8, 0, 4,
+       launch_gemm_bf16<256, 256, 32, 4, 2, 4, 16>},
+      {"gemm_bf16_256x128x64_r3_m16", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 128, 64, 8, 0, 3,
+       launch_gemm_bf16<256, 128, 64, 3, 4, 2, 16>},
+      {"gemm_bf16_128x128x64_r4_m16", TILEC_FAMILY_GEMM, TILEC_BF16, 128, 128, 64, 8, 0, 4,
+       launch_gemm_bf16<128, 128, 64, 4, 2, 4, 16>},
+      {"gemm_bf16_256x256x64_r2_m16_kc", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 64, 8, 0, 2,
+       launch_gemm_bf16_kc<256, 256, 64, 2, 2, 4, 16>, 1},
+      {"gemm_bf16_256x256x32_r4w8_m16_kc", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 32, 8, 0, 4,
+       launch_gemm_bf16_kc<256, 256, 32, 4, 2, 4, 16>, 1},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

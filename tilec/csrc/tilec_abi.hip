@@ -198,7 +198,8 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
   // bf16: the streaming kernel for M <= 16 (it runs fp32 MFMAs on widened
   // inputs, so more rows are better served by the bf16 tile GEMMs).
   if (M <= 16 && skinny_fits(ldx1, ldx2, layout)) return find("skinny_bf16_w8_b1");
-  static const char* order[] = {"gemm_bf16_256x256x64_r2", "gemm_bf16_256x128x64_r3", "gemm_bf16_128x128x64_r4"};
+  static const char* order[] = {"gemm_bf16_256x256x64_r2_m16", "gemm_bf16_256x128x64_r3_m16",
+                                "gemm_bf16_128x128x64_r4"};
   for (const char* nm : order) {
     const int v = find(nm);
     const VariantDesc* d = table()[v];
