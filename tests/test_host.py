@@ -451,6 +451,29 @@ def test_scratch_query_follows_layout_and_strides():
     assert ext._scratch_sizes(8, 64, 200, 200, ld, 0, 0, -1, 0) == (ws, cnt)
 
 
+def test_pad_variants_offered_for_unaligned_rows_and_sized():
+    """The fp32 *_pad variants (both operands copied into the workspace with
+    rows padded to 16 bytes and K to the K step) are offered only where an
+    operand's rows are not whole 16-byte groups, and their scratch is the two
+    padded copies (each 256-byte aligned) plus the split-K partials."""
+    pads = lambda M, K, N, layout=0: {c for c in ext.hip_configs(M, K, N, "f32", layout) if c[0].endswith("_pad")}
+    assert pads(1000, 4097, 3001) and pads(3001, 513, 1000) and pads(1024, 1024, 1022)
+    assert not pads(1024, 1024, 1024) and not pads(4096, 4096, 4096)
+    assert not any(c[0].endswith("_pad") for c in ext.hip_configs(1000, 4097, 3001, "bf16"))
+    # layout: a column-major x1 is contiguous along M, a column-major x2 along K
+    assert ext.needs_pad(1001, 1024, 1024, _lib.X1_COL_MAJOR) and not ext.needs_pad(1001, 1024, 1024)
+    assert ext.needs_pad(1024, 1024, 1001) and not ext.needs_pad(1024, 1024, 1001, _lib.X2_COL_MAJOR)
+    vid = _lib.variant_id("gemm_f32_128x128x32_w2x4_pad")
+    M, N, K = 1000, 3001, 4097
+    kp, m4, n4 = 4128, 1000, 3004
+    copies = -(-m4 * kp * 4 // 256) * 256 + -(-n4 * kp * 4 // 256) * 256
+    rc, ws, cnt = _scratch(M, N, K, 0, 0, 0, variant=vid, split=1)
+    assert rc == _lib.OK and (ws, cnt) == (copies, 0)
+    tiles = 8 * 24
+    rc, ws, cnt = _scratch(M, N, K, 0, 0, 0, variant=vid, split=4)
+    assert rc == _lib.OK and ws == copies + 4 * tiles * 128 * 128 * 4 and cnt == tiles * 64 * 4
+
+
 def test_hip_configs_of_empty_outputs():
     for M, K, N in [(0, 64, 64), (4, 64, 0), (0, 0, 0)]:
         for dt in ("f32", "bf16"):

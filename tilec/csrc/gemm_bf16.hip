@@ -401,10 +401,6 @@ const VariantDesc* gemm_bf16_variants(int* count) {
        launch_gemm_bf16<256, 128, 64, 3, 4, 2, 16>},
       {"gemm_bf16_128x128x64_r4_m16", TILEC_FAMILY_GEMM, TILEC_BF16, 128, 128, 64, 8, 0, 4,
        launch_gemm_bf16<128, 128, 64, 4, 2, 4, 16>},
-      {"gemm_bf16_256x256x64_r2_m16_kc", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 64, 8, 0, 2,
-       launch_gemm_bf16_kc<256, 256, 64, 2, 2, 4, 16>, 1},
-      {"gemm_bf16_256x256x32_r4w8_m16_kc", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 32, 8, 0, 4,
-       launch_gemm_bf16_kc<256, 256, 32, 4, 2, 4, 16>, 1},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

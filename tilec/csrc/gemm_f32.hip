@@ -26,6 +26,7 @@
 //     edge tiles cost what interior ones do; otherwise clamped addresses plus
 //     selects on edge tiles and the K tail;
 //   * XCD-aware, grouped tile order (tile_of in common.h).
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -427,6 +428,111 @@ hipError_t launch_gemm_f32_unsplit(const MatmulArgs& a) {
   return launch_gemm_f32<64, 64, 16, 2, 2>(b);
 }
 
+// ---------------------------------------------------------------------------
+// Pad variants: each operand is first copied into the workspace with its
+// contiguous extent and row stride rounded up to 4 floats and K rounded up to
+// BK, zero-filled, so the direct-to-LDS kernel takes operands whose rows are
+// not 16-byte aligned (an odd K or N: the ragged BASELINE shapes run the
+// register-staged kernel otherwise).  The padding is zeros, so it adds
+// nothing to the product; C is written as the caller's M x N (the kernel's
+// column chunks past N may read padding, never store it).  Workspace:
+// [x1 padded][x2 padded][split-K partials], each 256-byte aligned.
+// ---------------------------------------------------------------------------
+
+// out (Rp x Cp, row stride Cp) = in (R x C, row stride ld) padded with zeros.
+// A thread writes 4 consecutive floats of one output row; Cp % 4 == 0 and the
+// output is 16-byte aligned.
+__global__ __launch_bounds__(256) void pad_copy_f32_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                           int R, int C, int64_t ld, int Rp, int Cp) {
+  const int c0 = 4 * (blockIdx.x * 256 + threadIdx.x);
+  if (c0 >= Cp) return;
+  for (int r = blockIdx.y; r < Rp; r += gridDim.y) {
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (r < R) {
+      const float* src = in + (int64_t)r * ld;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c0 + e < C) v[e] = src[c0 + e];
+    }
+    *reinterpret_cast<f32x4*>(out + (int64_t)r * Cp + c0) = v;
+  }
+}
+
+hipError_t pad_copy_f32(const float* in, float* out, int64_t R, int64_t C, int64_t ld, int64_t Rp, int64_t Cp,
+                        hipStream_t stream) {
+  if (Rp == 0 || Cp == 0) return hipSuccess;
+  const dim3 grid((unsigned)cdiv(Cp / 4, 256), (unsigned)std::min<int64_t>(Rp, 65535));
+  hipLaunchKernelGGL(pad_copy_f32_kernel, grid, dim3(256), 0, stream, in, out, (int)R, (int)C, ld, (int)Rp, (int)Cp);
+  return hipGetLastError();
+}
+
+// Padded extents: K up to the K step, the contiguous extent of a
+// column-major x1 (M) or a row-major x2 (N) up to 4.  Sized for either
+// layout, since the size queries do not see it.
+struct PadGeom {
+  int64_t kp, m4, n4;
+  size_t x1_bytes, x2_bytes;  // 256-byte aligned
+};
+inline PadGeom pad_geom(int64_t M, int64_t N, int64_t K, int64_t bk) {
+  PadGeom g;
+  g.kp = cdiv(K, bk) * bk;
+  g.m4 = cdiv(M, 4) * 4;
+  g.n4 = cdiv(N, 4) * 4;
+  g.x1_bytes = (size_t)cdiv(g.m4 * g.kp * 4, 256) * 256;
+  g.x2_bytes = (size_t)cdiv(g.n4 * g.kp * 4, 256) * 256;
+  return g;
+}
+
+size_t pad_workspace_bytes(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
+  if (M == 0 || N == 0 || K == 0) return 0;
+  const PadGeom p = pad_geom(M, N, K, d.bk);
+  const SplitGeom g = gemm_split_geom(p.kp, d.bk, split_k);
+  const size_t partials = g.splits > 1 ? (size_t)g.splits * cdiv(M, d.bm) * cdiv(N, d.bn) * d.bm * d.bn * 4 : 0;
+  return p.x1_bytes + p.x2_bytes + partials;
+}
+size_t pad_counter_bytes(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
+  if (M == 0 || N == 0 || K == 0 || gemm_split_geom(K, d.bk, split_k).splits <= 1) return 0;
+  return (size_t)cdiv(M, d.bm) * cdiv(N, d.bn) * kSplitCounterStride * sizeof(unsigned);
+}
+
+template <int BM, int BN, int BK, int NBUF, int WM, int WN>
+hipError_t launch_gemm_f32_pad(const MatmulArgs& a) {
+  if (a.M == 0 || a.N == 0 || a.K == 0) return launch_gemm_f32_dma<BM, BN, BK, NBUF, WM, WN>(a);
+  const bool ca = a.layout & TILEC_X1_COL_MAJOR, cb = a.layout & TILEC_X2_COL_MAJOR;
+  const PadGeom p = pad_geom(a.M, a.N, a.K, BK);
+  // Stored (rows x cols) of each operand, before and after padding.
+  const int64_t r1 = ca ? a.K : a.M, c1 = ca ? a.M : a.K, r1p = ca ? p.kp : a.M, c1p = ca ? p.m4 : p.kp;
+  const int64_t r2 = cb ? a.N : a.K, c2 = cb ? a.K : a.N, r2p = cb ? a.N : p.kp, c2p = cb ? p.kp : p.n4;
+  // The direct-to-LDS kernel's per-step offsets: (strided rows of a tile) *
+  // ld * 4 < 2^31; beyond that the register-staged kernel on the operands
+  // as they are (its workspace use is only the split partials).
+  constexpr int64_t lim = (int64_t(1) << 31) - 4096;
+  if ((ca ? BK : BM) * c1p * 4 >= lim || (cb ? BN : BK) * c2p * 4 >= lim || r1p * c1p >= (int64_t(1) << 31) ||
+      r2p * c2p >= (int64_t(1) << 31) || reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0)
+    return launch_gemm_f32<BM, BN, BK, WM, WN>(a);
+  char* ws = static_cast<char*>(a.workspace);
+  float* x1p = reinterpret_cast<float*>(ws);
+  float* x2p = reinterpret_cast<float*>(ws + p.x1_bytes);
+  hipError_t e = pad_copy_f32(static_cast<const float*>(a.x1), x1p, r1, c1, a.ldx1, r1p, c1p, a.stream);
+  if (e != hipSuccess) return e;
+  e = pad_copy_f32(static_cast<const float*>(a.x2), x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
+  if (e != hipSuccess) return e;
+  MatmulArgs b = a;
+  b.x1 = x1p;
+  b.x2 = x2p;
+  b.K = p.kp;
+  b.ldx1 = c1p;
+  b.ldx2 = c2p;
+  b.workspace = ws + p.x1_bytes + p.x2_bytes;
+  b.workspace_bytes = a.workspace_bytes - p.x1_bytes - p.x2_bytes;
+  switch (a.layout & 3) {
+    case 0: return launch_gemm_f32_lds<BM, BN, BK, NBUF, WM, WN, false, false>(b);
+    case TILEC_X1_COL_MAJOR: return launch_gemm_f32_lds<BM, BN, BK, NBUF, WM, WN, true, false>(b);
+    case TILEC_X2_COL_MAJOR: return launch_gemm_f32_lds<BM, BN, BK, NBUF, WM, WN, false, true>(b);
+    default: return launch_gemm_f32_lds<BM, BN, BK, NBUF, WM, WN, true, true>(b);
+  }
+}
+
 // Variant table for this family (its order is part of the variant numbering).
 const VariantDesc* gemm_f32_variants(int* count) {
   static const VariantDesc t[] = {
@@ -463,6 +569,11 @@ const VariantDesc* gemm_f32_variants(int* count) {
        launch_gemm_f32_dma<64, 64, 32, 3, 2, 2>},
       {"gemm_f32_64x64x64_w2x2_lds", TILEC_FAMILY_GEMM, TILEC_F32, 64, 64, 64, 4, 0, 3,
        launch_gemm_f32_dma<64, 64, 64, 3, 2, 2>},
+      // operands padded into the workspace for the direct-to-LDS kernel
+      {"gemm_f32_128x128x32_w2x4_pad", TILEC_FAMILY_GEMM, TILEC_F32, 128, 128, 32, 8, 0, 3,
+       launch_gemm_f32_pad<128, 128, 32, 3, 2, 4>, 0, pad_workspace_bytes, pad_counter_bytes},
+      {"gemm_f32_64x64x32_w2x2_pad", TILEC_FAMILY_GEMM, TILEC_F32, 64, 64, 32, 4, 0, 3,
+       launch_gemm_f32_pad<64, 64, 32, 3, 2, 2>, 0, pad_workspace_bytes, pad_counter_bytes},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;
