@@ -49,14 +49,19 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // A k-contiguous stage: chunk c of row i is stored at (c ^ swz_a) within the
 // row; BK=64 rows are 128 B (8 chunks, 2 rows per 256-byte bank line), BK=32
-// rows 64 B (4 chunks).  An r-contiguous stage: chunks of k-row r are
-// swizzled by 4 * (r & 3), so the 8 rows one transposing read touches spread
-// over the banks.
-template <int BK>
+// rows 64 B (4 chunks), swizzled by rows (row >> 2) for the 32x32 blocks'
+// reads and (row >> 1) for the 16x16 blocks' (each measured free of bank
+// conflicts for its own read pattern, and conflicting for the other's).  An r-contiguous stage: chunks of k-row r are
+// swizzled by 4 * (r & 3) ^ 2 * ((r >> 3) & 1).  A transposing read serves 32
+// lanes per pass; with 32x32 blocks they read 4 k-rows x 32 columns (four
+// chunks, spread over all 64 banks by the first term), with 16x16 blocks two
+// groups of 4 k-rows 8 apart x 16 columns each: the second term moves the
+// upper group's chunks onto the banks the lower group leaves free.
+template <int BK, int MF>
 __device__ __forceinline__ int swz_a(int row) {
-  return BK == 64 ? (row >> 1) & 7 : (row >> 2) & 3;
+  return BK == 64 ? (row >> 1) & 7 : (row >> (MF == 16 ? 1 : 2)) & 3;
 }
-__device__ __forceinline__ int swz_b(int krow) { return 4 * (krow & 3); }
+__device__ __forceinline__ int swz_b(int krow) { return (4 * (krow & 3)) ^ (2 * ((krow >> 3) & 1)); }
 
 // How one operand's tile (R rows of its outer dimension — M for x1, N for
 // x2 — by BK of K) sits in a stage buffer.
@@ -66,7 +71,7 @@ __device__ __forceinline__ int swz_b(int krow) { return 4 * (krow & 3); }
 //   otherwise (r contiguous: row-major x2, column-major x1): BK rows of R
 //     elements, chunks swizzled by swz_b; a fragment comes from two
 //     ds_read_b64_tr_b16 transposing reads.
-template <int R, int BK, int NW, bool KC>
+template <int R, int BK, int NW, bool KC, int MF>
 struct Stage {
   static constexpr bool kKC = KC;
   static constexpr int ROW_CHUNKS = KC ? BK / 8 : R / 8;  // 16-byte chunks per stored row
@@ -76,7 +81,7 @@ struct Stage {
   static_assert(CHUNKS % (64 * NW) == 0, "DMA must divide evenly");
   static_assert(KC || R % 128 == 0, "transposed-read swizzle needs rows of >= 16 chunks");
   static_assert(!KC || BK == 32 || BK == 64, "row swizzle covers 4 or 8 chunks per row");
-  __device__ __forceinline__ static int swz(int row) { return KC ? swz_a<BK>(row) : swz_b(row); }
+  __device__ __forceinline__ static int swz(int row) { return KC ? swz_a<BK, MF>(row) : swz_b(row); }
   // Stored row and logical chunk of physical chunk p.
   __device__ __forceinline__ static void chunk(int p, int& row, int& lc) {
     row = p / ROW_CHUNKS;
@@ -98,8 +103,8 @@ struct LdsGemm {
   static constexpr int KS = BK / (8 * KG);     // MFMA k-slices per step
   static constexpr int ACC = MF * MF / 64;     // accumulator floats per lane per block
   using Acc = std::conditional_t<MF == 32, f32x16, f32x4>;
-  using SA = Stage<BM, BK, NW, !CA>;
-  using SB = Stage<BN, BK, NW, CB>;
+  using SA = Stage<BM, BK, NW, !CA, MF>;
+  using SB = Stage<BN, BK, NW, CB, MF>;
   static constexpr int A_INSTR = SA::INSTR, B_INSTR = SB::INSTR;
   static constexpr int IPS = A_INSTR + B_INSTR;
   static constexpr int A_BYTES = SA::BYTES, B_BYTES = SB::BYTES;
