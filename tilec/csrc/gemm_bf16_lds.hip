@@ -619,8 +619,10 @@ hipError_t launch_gemm_bf16_lds(const MatmulArgs& a) {
   if constexpr (MF == 16) {
     if (a.K % BK != 0) return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, CA, CB, 32>(a);
   }
-  auto kern = a.K % BK == 0 || MF == 16 ? gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, true, CA, CB, MF>
-                                        : gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, false, CA, CB, MF>;
+  auto kern = gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, true, CA, CB, MF>;
+  if constexpr (MF == 32) {
+    if (a.K % BK != 0) kern = gemm_bf16_lds_kernel<BM, BN, BK, NBUF, WM, WN, false, CA, CB, MF>;
+  }
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)g.splits), dim3(P::NT), 0, a.stream,
                      static_cast<const u16*>(a.x1), static_cast<const u16*>(a.x2), a.out, (int)a.M, (int)a.N,
                      (int)a.K, a.ldx1, a.ldx2, a.ldo, 4, device_xcds(), (int)g.steps, g.splits > 1 ? static_cast<float*>(a.workspace) : nullptr,
