@@ -113,6 +113,8 @@ struct LdsGemm {
   static_assert(WTM % MF == 0 && WTN % MF == 0, "wave tile must be whole MFMA blocks");
   static_assert(MF == 16 || KS % 2 == 0, "a step's last k-slice ends in the second fragment set");
   static_assert(KS % 2 == 0 || NBUF % 2 == 0, "odd k-slice counts alternate fragment sets by step parity");
+  // 16x16 pipeline: one B fragment set for an even k-slice count.
+  static constexpr bool B1 = KS % 2 == 0;
   static_assert(NBUF >= 2 && NBUF <= 4, "ring of 2..4 stage buffers");
   static_assert((size_t)NBUF * STAGE_BYTES <= 160 * 1024, "LDS is 160 KiB");
   static_assert((NBUF - 2) * IPS <= 63, "vmcnt is 6 bits");
@@ -149,12 +151,13 @@ __device__ __forceinline__ void sched_mfma_vmem() {
 }
 
 // Scheduling groups for the 16x16 pipeline: the B reads of the next k-slice
-// (TN fragments of RB reads) first, then per row block x: 1 MFMA, its share of
-// IPS loads, the other TN - 1 MFMAs, the RA reads refilling its A fragment.
+// (TN fragments of RB reads; RB = 0 when they follow instead) first, then per
+// row block x: 1 MFMA, its share of IPS loads, the other TN - 1 MFMAs, the RA
+// reads refilling its A fragment.
 template <int TM, int TN, int IPS, int RA, int RB, int X = -1>
 __device__ __forceinline__ void sched_rows() {
   if constexpr (X < 0) {
-    __builtin_amdgcn_sched_group_barrier(0x100, TN * RB, 0);
+    if constexpr (RB > 0) __builtin_amdgcn_sched_group_barrier(0x100, TN * RB, 0);
     sched_rows<TM, TN, IPS, RA, RB, 0>();
   } else if constexpr (X < TM) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -464,25 +467,29 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
   mma(f[1]);  // last k-slice of the last step (zeros if K == 0)
   } else {
     // 16x16x32 blocks: a k-slice's fragments take twice the registers of a
-    // 32x32x16 slice for the same wave tile, so only B keeps two sets.  A has
-    // one: right after the MFMAs of row block x are issued, fa[x] is refilled
-    // from the next k-slice.  Entering step kt (its stage landed everywhere):
-    // fa and fb[1] hold the last k-slice of step kt-1, MFMAs not yet issued
-    // (zeros before step 0).  Step kt:
-    //   1. read B of k-slice 0 into fb[0];
-    //   2. MFMAs of (fa, fb[1]), row block by row block, each followed by its
-    //      refill from k-slice 0, with the loads of step kt+NBUF-1 threaded
+    // 32x32x16 slice for the same wave tile.  A has one set: right after the
+    // MFMAs of row block x are issued, fa[x] is refilled from the next
+    // k-slice.  B has one set too when a step has an even number of k-slices
+    // (read right after the MFMAs that used the previous slice); 32-deep steps
+    // (one k-slice) keep two B sets, read a step ahead.  Entering step kt (its stage landed everywhere):
+    // Entering step kt (its stage landed everywhere), fa and one B set hold
+    // the last k-slice of step kt-1, MFMAs not yet issued (zeros before step
+    // 0).  Step kt, an even number of k-slices:
+    //   1. MFMAs of (fa, fb[0]), row block by row block, each followed by its
+    //      A refill from k-slice 0, with the loads of step kt+NBUF-1 threaded
     //      between them (into the slot step kt-1 used; every wave finished
-    //      reading it before the last barrier);
-    //   3. per further k-slice ks: read B of ks into the other set, then the
-    //      MFMAs of (fa, the set of ks - 1), each row block refilled from ks;
-    //   4. wait for every read of this stage and for this wave's loads of
+    //      reading it before the last barrier); then read B of k-slice 0 into
+    //      fb[0];
+    //   2. per further k-slice ks: the MFMAs of k-slice ks-1, each row block
+    //      refilled from ks, then B of ks into fb[0];
+    //   3. wait for every read of this stage and for this wave's loads of
     //      step kt+1, then the barrier.
-    // The previous step's last B is in fb[1] for an even slice count; for an
-    // odd one the sets alternate by step parity (ring slot i = step % NBUF,
-    // NBUF even) and the step count is rounded up to even, so the last step's
-    // ends in fb[0]: the extra step's stage holds zeros (its copies were
-    // issued past nk, with zero records) and adds nothing.
+    // One k-slice per step (BK = 32): B of the step's k-slice is read into
+    // the set the previous step's MFMAs do not use, before them; the sets
+    // alternate by step parity (ring slot i = step % NBUF, NBUF even) and the
+    // step count is rounded up to even, so the last step's ends in fb[0]: the
+    // extra step's stage holds zeros (its copies were issued past nk, with
+    // zero records) and adds nothing.
     bf16x8 fa[P::TM], fb[2][P::TN];
 #pragma unroll
     for (int i = 0; i < P::TM; ++i) fa[i] = bf16x8{};
@@ -501,7 +508,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
         for (int j = 0; j < P::TN; ++j) acc[x][j] = mfma_blk(fa[x], b[j], acc[x][j]);
         fa[x] = frag(SA{}, st, a_r[x], tr_a[x], ks);
       }
-      sched_rows<P::TM, P::TN, 0, RA, RB>();
+      sched_rows<P::TM, P::TN, 0, RA, P::B1 ? 0 : RB>();
     };
     auto mma_refill_dma = [&](const bf16x8 (&b)[P::TN], const char* st, int kt, char* dst)
         __attribute__((always_inline)) {
@@ -518,20 +525,30 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
         }
         fa[x] = frag(SA{}, st, a_r[x], tr_a[x], 0);
       }
-      sched_rows<P::TM, P::TN, P::IPS, RA, RB>();
+      sched_rows<P::TM, P::TN, P::IPS, RA, P::B1 ? 0 : RB>();
     };
     auto step16 = [&](auto I, int kt) __attribute__((always_inline)) {
       constexpr int i = decltype(I)::value;
-      constexpr int pv = KS % 2 == 0 ? 1 : (i & 1);  // set holding the previous step's last B
+      constexpr int pv = P::B1 ? 1 : (i & 1);  // set holding the previous step's last B
       constexpr int s0 = pv ^ 1;                     // set receiving k-slice 0's B
       char* const cur = buf(I);
-      read_b(cur, 0, fb[s0]);
-      mma_refill_dma(fb[pv], cur, kt + NBUF - 1, buf(std::integral_constant<int, (i + NBUF - 1) % NBUF>{}));
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (P::B1) {
+        // One B set: each k-slice's B is read right after the MFMAs that
+        // used the previous one were issued.
+        mma_refill_dma(fb[0], cur, kt + NBUF - 1, buf(std::integral_constant<int, (i + NBUF - 1) % NBUF>{}));
+        __builtin_amdgcn_sched_barrier(0);
+        read_b(cur, 0, fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int ks = 1; ks < KS; ++ks) {
-        read_b(cur, ks, fb[s0 ^ (ks & 1)]);
-        mma_refill(fb[s0 ^ ((ks - 1) & 1)], cur, ks);
+        for (int ks = 1; ks < KS; ++ks) {
+          mma_refill(fb[0], cur, ks);
+          __builtin_amdgcn_sched_barrier(0);
+          read_b(cur, ks, fb[0]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        read_b(cur, 0, fb[s0]);
+        mma_refill_dma(fb[pv], cur, kt + NBUF - 1, buf(std::integral_constant<int, (i + NBUF - 1) % NBUF>{}));
         __builtin_amdgcn_sched_barrier(0);
       }
       // vmcnt(WAIT) lgkmcnt(0) (gfx9 encoding, expcnt unconstrained)
@@ -539,7 +556,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
       step_barrier();
       __builtin_amdgcn_sched_barrier(0);
     };
-    const int nrun = KS % 2 == 0 ? nk : nk + (nk & 1);
+    const int nrun = P::B1 ? nk : nk + (nk & 1);
     if (nrun > 0) {
       dma(0, lds0);
       if constexpr (NBUF > 2) dma(1, lds1);
@@ -566,7 +583,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_bf16_lds_kernel(
 #pragma unroll
         for (int j = 0; j < P::TN; ++j) acc[x][j] = mfma_blk(fa[x], b[j], acc[x][j]);
     };
-    mma_last(fb[KS % 2 == 0 ? 1 : 0]);
+    mma_last(fb[0]);
   }
   // Loads issued for steps past K still write (zeros) into LDS: let them
   // land before this workgroup can finish and release its LDS.
