@@ -669,6 +669,51 @@ def test_f32_lds_copies_strides_and_fallbacks():
                         assert O.rel_l2(got, ref) <= O.TOL_F32, (v["name"], s, layout, pad, (m, k, n))
 
 
+def _view_at(x, col, off, extra):
+    """The [r, c] device matrix x copied into a flat buffer at element offset
+    `off`, row-major (or column-major when col) with a leading dimension
+    `extra` elements longer than needed."""
+    r, c = x.shape
+    ld = (r if col else c) + extra
+    flat = torch.zeros(off + ld * (c if col else r) + 1, dtype=x.dtype, device=x.device)
+    v = flat[off:].as_strided((r, c), (1, ld) if col else (ld, 1))
+    v.copy_(x)
+    return v
+
+
+def test_pad_variants_any_alignment():
+    """The pad variants (operands copied into the workspace with 16-byte rows,
+    every row's bytes shifted into place) on operands at every element
+    misalignment of base and row stride, in every layout, K splits where the
+    tile splits: the fp64 oracle, and small integers exactly."""
+    pads = [v for v in _lib.variants() if v["name"].endswith("_pad")]
+    assert len(pads) == 5
+    shapes = [(67, 1001, 93), (130, 515, 264), (5, 77, 9), (300, 200, 131)]
+    for i, (m, k, n) in enumerate(shapes):
+        a, b = O.normal((m, k), 1400 + 2 * i), O.normal((k, n), 1401 + 2 * i)
+        ai, bi = O.small_ints((m, k), 1420 + 2 * i, -3, 3), O.small_ints((k, n), 1421 + 2 * i, -3, 3)
+        want = (ai.astype(np.int64) @ bi.astype(np.int64)).astype(np.float32)
+        for v in pads:
+            bf16 = v["dtype"] == _lib.BF16
+            if bf16:
+                a16, b16 = O.bf16_round(a), O.bf16_round(b)
+                x1, x2, ref, tol = dev_bf16(a16), dev_bf16(b16), O.matmul_bf16_f64(a16, b16), 1e-5
+                y1, y2 = dev(ai, torch.bfloat16), dev(bi, torch.bfloat16)
+            else:
+                x1, x2, ref, tol = dev(a), dev(b), O.matmul_f64(a, b), O.TOL_F32
+                y1, y2 = dev(ai), dev(bi)
+            splits = [1, 3] if ext.tile_can_split(v) and i == 0 else [1]
+            for layout in [0] + LAYOUTS:
+                c1, c2 = bool(layout & _lib.X1_COL_MAJOR), bool(layout & _lib.X2_COL_MAJOR)
+                for off, extra in ((1, 3), (3, 0), (0, 5), (2, 1)):
+                    for s in splits:
+                        say(f"{v['name']} split {s} layout {layout} offset {off} extra {extra} shape {(m, k, n)}")
+                        got = run(_view_at(x1, c1, off, extra), _view_at(x2, c2, off + 1, extra), (v["name"], s))
+                        assert O.rel_l2(got, ref) <= tol, (v["name"], s, layout, off, extra, (m, k, n))
+                        got = run(_view_at(y1, c1, off, extra), _view_at(y2, c2, off + 1, extra), (v["name"], s))
+                        np.testing.assert_array_equal(got, want)
+
+
 def test_layouts_padded_strides_and_splits():
     """Column strides above the row count, and K splits of the tile GEMMs,
     in every layout."""

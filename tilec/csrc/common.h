@@ -7,6 +7,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
 
 namespace tilec {
@@ -372,6 +373,75 @@ __device__ __forceinline__ void tile_of(int bid, int xcds, int tiles_m, int tile
   const int in_g = lid - g * per_group;
   tm = first_m + in_g % gsize;
   tn = in_g / gsize;
+}
+
+// ---------------------------------------------------------------------------
+// Padding copy of the pad variants (gemm_f32.hip, gemm_bf16.hip): out (Rp x
+// Cp, row stride Cp) = in (R x C, row stride ld) with zeros past R and C, for
+// ESZ-byte elements at any element alignment of `in` and ld.  A thread
+// writes one 16-byte chunk of an output row.  It reads the 16-byte aligned
+// chunk of the input row holding the chunk's first element and, where the
+// chunk's bytes run into it, the next aligned chunk, then shifts the bytes
+// into place (v_alignbyte on a dword window chosen by the row's byte
+// misalignment).  Every load holds at least one byte of the row it serves,
+// so no access leaves that row's own 16-byte chunks: nothing past the
+// matrix, no page the matrix does not touch.  Rows of 2^LG threads: narrow
+// outputs pack 256 >> LG rows per workgroup.  Cp * ESZ % 16 == 0 and `out`
+// is 16-byte aligned.
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int ESZ>
+__global__ __launch_bounds__(256) void pad_copy_kernel(const unsigned char* __restrict__ in,
+                                                       unsigned char* __restrict__ out, int64_t R, int64_t C,
+                                                       int64_t ld, int64_t Rp, int64_t Cp, int lg) {
+  constexpr int EPC = 16 / ESZ;  // elements per 16-byte chunk
+  const int64_t nch = Cp / EPC;
+  const int64_t ch = (int64_t)blockIdx.x * (1 << lg) + (threadIdx.x & ((1 << lg) - 1));
+  const int64_t rpb = 256 >> lg;  // rows per workgroup
+  const int64_t c0 = ch * EPC;
+  if (ch >= nch) return;
+  for (int64_t r = (int64_t)blockIdx.y * rpb + (threadIdx.x >> lg); r < Rp; r += (int64_t)gridDim.y * rpb) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r < R && c0 < C) {
+      const uintptr_t start = reinterpret_cast<uintptr_t>(in) + (uintptr_t)(r * ld * ESZ);
+      const uint32_t b = (uint32_t)(start & 15);  // the row's byte misalignment
+      const uintptr_t lo = start - b + (uintptr_t)(c0 * ESZ);
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(lo);
+      u32x4 a1 = {0u, 0u, 0u, 0u};
+      if (b != 0 && c0 * ESZ + 16 < (int64_t)b + C * ESZ) a1 = *reinterpret_cast<const u32x4*>(lo + 16);
+      const uint32_t d[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const uint32_t w = b >> 2, rb = b & 3;
+      uint32_t e[5];
+#pragma unroll
+      for (int j = 0; j < 5; ++j) e[j] = w == 0 ? d[j] : w == 1 ? d[j + 1] : w == 2 ? d[j + 2] : d[j + 3];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = __builtin_amdgcn_alignbyte(e[j + 1], e[j], rb);
+      if (c0 + EPC > C) {  // the row's last chunk: zero the elements past C
+        const int keep = (int)(C - c0) * ESZ;  // bytes kept
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int kb = keep - 4 * j;
+          v[j] = kb >= 4 ? v[j] : kb <= 0 ? 0u : (v[j] & ((1u << (8 * kb)) - 1u));
+        }
+      }
+    }
+    *reinterpret_cast<u32x4*>(out + (r * Cp + c0) * ESZ) = v;
+  }
+}
+
+template <int ESZ>
+inline hipError_t pad_copy(const void* in, void* out, int64_t R, int64_t C, int64_t ld, int64_t Rp, int64_t Cp,
+                           hipStream_t stream) {
+  if (Rp == 0 || Cp == 0) return hipSuccess;
+  const int64_t nch = Cp / (16 / ESZ);
+  int lg = 0;
+  while (lg < 8 && (int64_t(1) << lg) < nch) ++lg;
+  const int64_t rpb = 256 >> lg;
+  const dim3 grid((unsigned)((nch + (1 << lg) - 1) >> lg), (unsigned)std::min<int64_t>((Rp + rpb - 1) / rpb, 65535));
+  hipLaunchKernelGGL(pad_copy_kernel<ESZ>, grid, dim3(256), 0, stream, static_cast<const unsigned char*>(in),
+                     static_cast<unsigned char*>(out), R, C, ld, Rp, Cp, lg);
+  return hipGetLastError();
 }
 
 }  // namespace tilec

@@ -363,6 +363,88 @@ hipError_t launch_gemm_bf16_kc(const MatmulArgs& a) {
   return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, false, true, MF>(b);
 }
 
+// ---------------------------------------------------------------------------
+// Pad variants: an operand whose rows are not whole 16-byte groups (its
+// contiguous extent or row stride not a multiple of 8 elements, e.g. an odd
+// K) cannot take the LDS-DMA kernel's 16-byte copies, and the plain variants
+// run the generic kernel for it (2-3x slower on MI355X).  These variants
+// first copy both operands into the workspace in the caller's layout, the
+// contiguous extent and row stride rounded up to 8 elements and K up to the
+// K step, zero-filled, then run the LDS-DMA kernel on the copies.  Zeros add
+// nothing to the product; C is written as the caller's M x N (column chunks
+// past N may read padding, never store it).  Workspace: [x1 padded][x2
+// padded][split-K partials], each 256-byte aligned.  The copies are
+// common.h's pad_copy.
+// ---------------------------------------------------------------------------
+
+// Padded extents: K up to the K step, the contiguous extent of a
+// column-major x1 (M) or a row-major x2 (N) up to 8.  Sized for either
+// layout, since the size queries do not see it.
+struct PadGeomBf16 {
+  int64_t kp, m8, n8;
+  size_t x1_bytes, x2_bytes;  // 256-byte aligned
+};
+inline PadGeomBf16 pad_geom_bf16(int64_t M, int64_t N, int64_t K, int64_t bk) {
+  PadGeomBf16 g;
+  g.kp = cdiv(K, bk) * bk;
+  g.m8 = cdiv(M, 8) * 8;
+  g.n8 = cdiv(N, 8) * 8;
+  g.x1_bytes = (size_t)cdiv(g.m8 * g.kp * 2, 256) * 256;
+  g.x2_bytes = (size_t)cdiv(g.n8 * g.kp * 2, 256) * 256;
+  return g;
+}
+
+size_t pad_workspace_bytes_bf16(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
+  if (M == 0 || N == 0 || K == 0) return 0;
+  const PadGeomBf16 p = pad_geom_bf16(M, N, K, d.bk);
+  const SplitGeom g = gemm_split_geom(p.kp, d.bk, split_k);
+  const size_t partials = g.splits > 1 ? (size_t)g.splits * cdiv(M, d.bm) * cdiv(N, d.bn) * d.bm * d.bn * 4 : 0;
+  return p.x1_bytes + p.x2_bytes + partials;
+}
+size_t pad_counter_bytes_bf16(const VariantDesc& d, int64_t M, int64_t N, int64_t K, int split_k) {
+  if (M == 0 || N == 0 || K == 0 || gemm_split_geom(K, d.bk, split_k).splits <= 1) return 0;
+  return (size_t)cdiv(M, d.bm) * cdiv(N, d.bn) * kSplitCounterStride * sizeof(unsigned);
+}
+
+template <int BM, int BN, int BK, int NBUF, int WM, int WN, int MF>
+hipError_t launch_gemm_bf16_pad(const MatmulArgs& a) {
+  if (a.M == 0 || a.N == 0 || a.K == 0) return launch_gemm_bf16<BM, BN, BK, NBUF, WM, WN, MF>(a);
+  const bool ca = a.layout & TILEC_X1_COL_MAJOR, cb = a.layout & TILEC_X2_COL_MAJOR;
+  const PadGeomBf16 p = pad_geom_bf16(a.M, a.N, a.K, BK);
+  // Stored (rows x cols) of each operand, before and after padding.
+  const int64_t r1 = ca ? a.K : a.M, c1 = ca ? a.M : a.K, r1p = ca ? p.kp : a.M, c1p = ca ? p.m8 : p.kp;
+  const int64_t r2 = cb ? a.N : a.K, c2 = cb ? a.K : a.N, r2p = cb ? a.N : p.kp, c2p = cb ? p.kp : p.n8;
+  // The LDS-DMA kernel's byte offsets within one K step (strided rows of a
+  // tile times the row stride, as launch_layout checks them) and the copy
+  // kernel's 32-bit extents; beyond them the plain variant on the operands
+  // as they are (its workspace use is only the split partials).
+  constexpr int64_t lim = (int64_t(1) << 31) - 4096;
+  if ((ca ? BK : BM) * c1p * 2 >= lim || (cb ? BN : BK) * c2p * 2 >= lim || std::max(r1p, c1p) >= lim ||
+      std::max(r2p, c2p) >= lim || reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0)
+    return launch_gemm_bf16<BM, BN, BK, NBUF, WM, WN, MF>(a);
+  char* ws = static_cast<char*>(a.workspace);
+  u16* x1p = reinterpret_cast<u16*>(ws);
+  u16* x2p = reinterpret_cast<u16*>(ws + p.x1_bytes);
+  hipError_t e = pad_copy<2>(a.x1, x1p, r1, c1, a.ldx1, r1p, c1p, a.stream);
+  if (e != hipSuccess) return e;
+  e = pad_copy<2>(a.x2, x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
+  if (e != hipSuccess) return e;
+  MatmulArgs b = a;
+  b.x1 = x1p;
+  b.x2 = x2p;
+  b.K = p.kp;
+  b.ldx1 = c1p;
+  b.ldx2 = c2p;
+  b.workspace = ws + p.x1_bytes + p.x2_bytes;
+  b.workspace_bytes = a.workspace_bytes - p.x1_bytes - p.x2_bytes;
+  switch (a.layout & 3) {
+    case 0: return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, false, false, MF>(b);
+    case TILEC_X1_COL_MAJOR: return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, true, false, MF>(b);
+    case TILEC_X2_COL_MAJOR: return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, false, true, MF>(b);
+    default: return launch_gemm_bf16_lds<BM, BN, BK, NBUF, WM, WN, true, true, MF>(b);
+  }
+}
+
 }  // namespace
 
 // Variant table for this family (its order is part of the variant numbering).
@@ -401,6 +483,13 @@ const VariantDesc* gemm_bf16_variants(int* count) {
        launch_gemm_bf16<256, 128, 64, 3, 4, 2, 16>},
       {"gemm_bf16_128x128x64_r4_m16", TILEC_FAMILY_GEMM, TILEC_BF16, 128, 128, 64, 8, 0, 4,
        launch_gemm_bf16<128, 128, 64, 4, 2, 4, 16>},
+      // operands padded into the workspace for the LDS-DMA kernel
+      {"gemm_bf16_256x256x64_r2_m16_pad", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 256, 64, 8, 0, 2,
+       launch_gemm_bf16_pad<256, 256, 64, 2, 2, 4, 16>, 0, pad_workspace_bytes_bf16, pad_counter_bytes_bf16},
+      {"gemm_bf16_256x128x64_r3_m16_pad", TILEC_FAMILY_GEMM, TILEC_BF16, 256, 128, 64, 8, 0, 3,
+       launch_gemm_bf16_pad<256, 128, 64, 3, 4, 2, 16>, 0, pad_workspace_bytes_bf16, pad_counter_bytes_bf16},
+      {"gemm_bf16_128x128x64_r4_m16_pad", TILEC_FAMILY_GEMM, TILEC_BF16, 128, 128, 64, 8, 0, 4,
+       launch_gemm_bf16_pad<128, 128, 64, 4, 2, 4, 16>, 0, pad_workspace_bytes_bf16, pad_counter_bytes_bf16},
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

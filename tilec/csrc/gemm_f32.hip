@@ -436,35 +436,9 @@ hipError_t launch_gemm_f32_unsplit(const MatmulArgs& a) {
 // register-staged kernel otherwise).  The padding is zeros, so it adds
 // nothing to the product; C is written as the caller's M x N (the kernel's
 // column chunks past N may read padding, never store it).  Workspace:
-// [x1 padded][x2 padded][split-K partials], each 256-byte aligned.
+// [x1 padded][x2 padded][split-K partials], each 256-byte aligned.  The
+// copies are common.h's pad_copy.
 // ---------------------------------------------------------------------------
-
-// out (Rp x Cp, row stride Cp) = in (R x C, row stride ld) padded with zeros.
-// A thread writes 4 consecutive floats of one output row; Cp % 4 == 0 and the
-// output is 16-byte aligned.
-__global__ __launch_bounds__(256) void pad_copy_f32_kernel(const float* __restrict__ in, float* __restrict__ out,
-                                                           int R, int C, int64_t ld, int Rp, int Cp) {
-  const int c0 = 4 * (blockIdx.x * 256 + threadIdx.x);
-  if (c0 >= Cp) return;
-  for (int r = blockIdx.y; r < Rp; r += gridDim.y) {
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (r < R) {
-      const float* src = in + (int64_t)r * ld;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (c0 + e < C) v[e] = src[c0 + e];
-    }
-    *reinterpret_cast<f32x4*>(out + (int64_t)r * Cp + c0) = v;
-  }
-}
-
-hipError_t pad_copy_f32(const float* in, float* out, int64_t R, int64_t C, int64_t ld, int64_t Rp, int64_t Cp,
-                        hipStream_t stream) {
-  if (Rp == 0 || Cp == 0) return hipSuccess;
-  const dim3 grid((unsigned)cdiv(Cp / 4, 256), (unsigned)std::min<int64_t>(Rp, 65535));
-  hipLaunchKernelGGL(pad_copy_f32_kernel, grid, dim3(256), 0, stream, in, out, (int)R, (int)C, ld, (int)Rp, (int)Cp);
-  return hipGetLastError();
-}
 
 // Padded extents: K up to the K step, the contiguous extent of a
 // column-major x1 (M) or a row-major x2 (N) up to 4.  Sized for either
@@ -513,9 +487,9 @@ hipError_t launch_gemm_f32_pad(const MatmulArgs& a) {
   char* ws = static_cast<char*>(a.workspace);
   float* x1p = reinterpret_cast<float*>(ws);
   float* x2p = reinterpret_cast<float*>(ws + p.x1_bytes);
-  hipError_t e = pad_copy_f32(static_cast<const float*>(a.x1), x1p, r1, c1, a.ldx1, r1p, c1p, a.stream);
+  hipError_t e = pad_copy<4>(a.x1, x1p, r1, c1, a.ldx1, r1p, c1p, a.stream);
   if (e != hipSuccess) return e;
-  e = pad_copy_f32(static_cast<const float*>(a.x2), x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
+  e = pad_copy<4>(a.x2, x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
   if (e != hipSuccess) return e;
   MatmulArgs b = a;
   b.x1 = x1p;

@@ -103,7 +103,7 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             continue
         if panel_variant(v) and layout is not None and layout & _lib.X2_COL_MAJOR:
             continue  # the panel kernel reads a row-major x2 (it runs the streaming kernel otherwise)
-        if pad_variant(v) and not needs_pad(M, K, N, layout):
+        if pad_variant(v) and not needs_pad(M, K, N, layout, code):
             continue  # aligned operands: the direct-to-LDS variants read them in place
         if v["family"] == _lib.FAMILY_SKINNY and rows_variant(v):
             epl = 4 if code == _lib.F32 else 8  # elements per 16-byte load
@@ -177,19 +177,21 @@ def panel_variant(v):
 def pad_variant(v):
     """Variants named *_pad copy both operands into the workspace with rows
     padded to 16 bytes and K to the K step (zeros), then run the
-    direct-to-LDS tile kernel (csrc/gemm_f32.hip, launch_gemm_f32_pad)."""
+    direct-to-LDS tile kernel (csrc/gemm_f32.hip, launch_gemm_f32_pad;
+    csrc/gemm_bf16.hip, launch_gemm_bf16_pad)."""
     return v["name"].endswith("_pad")
 
 
-def needs_pad(M, K, N, layout=None):
-    """Whether an operand's rows are not whole 16-byte groups of fp32 (the
-    contiguous extent K of a row-major x1 or of a column-major x2, M of a
-    column-major x1, N of a row-major x2), so the direct-to-LDS tile
-    variants would run their register-staged kernel."""
+def needs_pad(M, K, N, layout=None, dtype="f32"):
+    """Whether an operand's rows are not whole 16-byte groups (4 fp32 or 8
+    bf16 elements) along its contiguous extent (K of a row-major x1 or of a
+    column-major x2, M of a column-major x1, N of a row-major x2), so the
+    direct-to-LDS tile variants would run their slower fallback kernel."""
     layout = layout or 0
+    epl = 4 if _dtype_code_name(dtype) == _lib.F32 else 8
     run1 = M if layout & _lib.X1_COL_MAJOR else K
     run2 = K if layout & _lib.X2_COL_MAJOR else N
-    return run1 % 4 != 0 or run2 % 4 != 0
+    return run1 % epl != 0 or run2 % epl != 0
 
 
 def prep_variant(v):
