@@ -184,31 +184,61 @@ def test_row_dot_configs_only_where_the_kernel_runs():
 
 def test_tune_features_and_shapes():
     f = tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8)
-    assert len(f) == 30 and all(math.isfinite(x) for x in f) and f[16:18] == [0.0, 0.0] and f[28:] == [1.0, 1.0]
+    assert len(f) == 34 and all(math.isfinite(x) for x in f) and f[16:18] == [0.0, 0.0] and f[28:30] == [1.0, 1.0]
     # alignment of each operand's contiguous extent: x1 row-major runs along K, x2 column-major along K
-    assert tune.features(5, 4097, 4096, 256, "f32", "skinny_f32_w8_b1", 1)[28:] == [0.0, 1.0]
-    assert tune.features(5, 4096, 4100, 256, "bf16", "skinny_bf16_w8_b1", 1)[28:] == [1.0, 0.0]
-    assert tune.features(6, 4096, 4100, 256, "bf16", "skinny_bf16_w8_b1", 1, layout=3)[28:] == [0.0, 1.0]
+    assert tune.features(5, 4097, 4096, 256, "f32", "skinny_f32_w8_b1", 1)[28:30] == [0.0, 1.0]
+    assert tune.features(5, 4096, 4100, 256, "bf16", "skinny_bf16_w8_b1", 1)[28:30] == [1.0, 0.0]
+    assert tune.features(6, 4096, 4100, 256, "bf16", "skinny_bf16_w8_b1", 1, layout=3)[28:30] == [0.0, 1.0]
+    # variant properties beyond the descriptor: 16x16 MFMA blocks, transposing and padding prepasses
+    assert f[30:33] == [0.0, 0.0, 0.0]
+    assert tune.features(4096, 4096, 4096, 256, "bf16", "gemm_bf16_256x256x64_r2_m16", 1)[30:33] == [1.0, 0.0, 0.0]
+    assert tune.features(4096, 4096, 4096, 256, "bf16", "gemm_bf16_256x256x64_r2_kc", 1)[30:33] == [0.0, 1.0, 0.0]
+    assert tune.features(1000, 4097, 3001, 256, "f32", "gemm_f32_64x64x32_w2x2_pad", 1)[30:33] == [0.0, 0.0, 1.0]
+    # whether the config runs its tile's slower fallback for these operands
+    fb = lambda *a: tune.features(*a)[33]
+    assert fb(1000, 4097, 3001, 256, "f32", "gemm_f32_128x128x32_w2x4_lds", 1, 0) == 1.0
+    assert fb(1000, 4097, 3001, 256, "f32", "gemm_f32_128x128x32_w2x4_pad", 1, 0) == 0.0
+    assert fb(1000, 4097, 3001, 256, "f32", "gemm_f32_128x128x32_w2x4", 1, 0) == 0.0  # register-staged: its own kernel
+    assert fb(1024, 4096, 1020, 256, "bf16", "gemm_bf16_128x128x64_r4_m16", 1, 0) == 1.0  # N % 8
+    assert fb(1024, 4096, 1020, 256, "bf16", "gemm_bf16_128x128x64_r4_m16", 1, 1) == 1.0
+    assert fb(1020, 4096, 1024, 256, "bf16", "gemm_bf16_128x128x64_r4_m16", 1, 0) == 0.0  # M is no row extent here
+    assert fb(1020, 4096, 1024, 256, "bf16", "gemm_bf16_128x128x64_r4_m16", 1, 1) == 1.0  # ... but is here
+    # kc transposes only when M, N and K are multiples of 8, else runs the plain tile
+    assert fb(1024, 4096, 1020, 256, "bf16", "gemm_bf16_128x128x64_r4_kc", 1, 0) == 1.0
+    assert fb(1020, 4096, 1024, 256, "bf16", "gemm_bf16_128x128x64_r4_kc", 1, 0) == 0.0
+    assert fb(1024, 4096, 1024, 256, "bf16", "gemm_bf16_128x128x64_r4_kc", 1, 3) == 0.0
+    assert fb(1020, 4096, 1024, 256, "bf16", "gemm_bf16_64x64x64_w2x2", 1, 1) == 0.0
+    assert fb(16, 4097, 4096, 256, "f32", "skinny_f32_w8_b1", 1, 0) == 0.0
+    # copies before the GEMM enter the analytic time: a launch each and their bytes
+    assert tune.prepass(1000, 4097, 3001, "f32", "gemm_f32_64x64x32_w2x2_pad") == (2, 8 * (1000 * 4097 + 4097 * 3001))
+    assert tune.prepass(1024, 512, 640, "bf16", "gemm_bf16_128x128x64_r4_kc", 1) == (2, 4 * (1024 * 512 + 512 * 640))
+    assert tune.prepass(1024, 512, 640, "bf16", "gemm_bf16_128x128x64_r4_kc", 2) == (0, 0)
+    assert tune.prepass(1024, 512, 640, "bf16", "gemm_bf16_128x128x64_r4_kc", 0) == (1, 4 * 512 * 640)
+    assert tune.prepass(1020, 512, 640, "bf16", "gemm_bf16_128x128x64_r4_kc", 0) == (0, 0)
+    assert tune.prepass(1024, 512, 640, "bf16", "gemm_bf16_128x128x64_r4", 1) == (0, 0)
+    m16, plain = (tune.features(4096, 4096, 4096, 256, "bf16", k, 1) for k in
+                  ("gemm_bf16_256x256x64_r2_m16", "gemm_bf16_256x256x64_r2"))
+    assert m16[:30] == plain[:30] and m16 != plain
     assert tune.features(16, 4096, 4096, 256, "f32", "skinny_f32_w8_b1", 8, layout=3)[16:18] == [1.0, 1.0]
     assert tune.features(1, 4096, 4096, 256, "f32", "skinny_f32_v1_w4_b2", 4)[18] == 1.0
-    s = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6, n_medium=0, n_narrow=0)
-    assert s == tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6, n_medium=0, n_narrow=0)
+    s = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6, n_medium=0, n_narrow=0, n_bf16=0)
+    assert s == tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6, n_medium=0, n_narrow=0, n_bf16=0)
     rm = [x for x in s if x[4] == 0]
     lay = [x for x in s if x[4] != 0]
     assert len(rm) == 120 + len(tune.CONFIG_SHAPES) and len(lay) == 40 + len(tune.LAYOUT_CONFIG_SHAPES) + 10 + 6
     # the x @ W.T streams (M <= 4 and 5 <= M <= 16, x2 column-major) add to, and do not change, the others
-    no_rows = tune.shapes(120, seed=0, n_layout=40, n_rows=0, n_tile=6, n_medium=0, n_narrow=0)
+    no_rows = tune.shapes(120, seed=0, n_layout=40, n_rows=0, n_tile=6, n_medium=0, n_narrow=0, n_bf16=0)
     assert set(no_rows) <= set(s) and all(x[0] <= 4 and x[4] == 2 for x in set(s) - set(no_rows))
-    no_tile = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=0, n_medium=0, n_narrow=0)
+    no_tile = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=0, n_medium=0, n_narrow=0, n_bf16=0)
     assert set(no_tile) <= set(s) and all(5 <= x[0] <= 16 and x[4] == 2 for x in set(s) - set(no_tile))
     assert {x + (0,) for x in tune.CONFIG_SHAPES} <= set(rm) and set(tune.LAYOUT_CONFIG_SHAPES) <= set(lay)
     assert {x[4] for x in lay} == {1, 2, 3}
     assert any(m <= 16 for m, *_ in s) and any(d == "bf16" for _, _, _, d, _ in s)
     # the row-major draws do not depend on the layout stream
-    assert rm == [x for x in tune.shapes(120, seed=0, n_layout=5, n_medium=0, n_narrow=0) if x[4] == 0]
+    assert rm == [x for x in tune.shapes(120, seed=0, n_layout=5, n_medium=0, n_narrow=0, n_bf16=0) if x[4] == 0]
     # the medium and narrow streams add row-major shapes in their ranges, and
     # never a shape the tuner must leave unseen
-    full = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6)
+    full = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6, n_bf16=0)
     more = set(full) - set(s)
     assert set(s) <= set(full) and 100 <= len(more) <= 140 and all(x[4] == 0 for x in more)
     for M, K, N, d, _ in more:
@@ -216,6 +246,11 @@ def test_tune_features_and_shapes():
         assert (48 <= small <= 600 and 500 <= large <= 6000 and 500 <= K <= 4096) or \
             (48 <= small <= 400 and 500 <= large <= 5000 and 2048 <= K <= 16384), (M, K, N)
     assert {d for *_, d, _ in more} == {"f32", "bf16"}
+    # the bf16 stream adds bf16 tile GEMMs in every layout, within its ranges
+    with_bf16 = tune.shapes(120, seed=0, n_layout=40, n_rows=10, n_tile=6)
+    extra = set(with_bf16) - set(full)
+    assert set(full) <= set(with_bf16) and 70 <= len(extra) <= 80 and {x[4] for x in extra} == {0, 1, 2, 3}
+    assert all(d == "bf16" and 64 <= M <= 8192 and 256 <= K <= 8192 and 64 <= N <= 8192 for M, K, N, d, _ in extra)
     assert not {u + (0,) for u in tune.UNSEEN_SHAPES} & set(tune.shapes(400))
 
 
@@ -459,7 +494,11 @@ def test_pad_variants_offered_for_unaligned_rows_and_sized():
     pads = lambda M, K, N, layout=0: {c for c in ext.hip_configs(M, K, N, "f32", layout) if c[0].endswith("_pad")}
     assert pads(1000, 4097, 3001) and pads(3001, 513, 1000) and pads(1024, 1024, 1022)
     assert not pads(1024, 1024, 1024) and not pads(4096, 4096, 4096)
-    assert not any(c[0].endswith("_pad") for c in ext.hip_configs(1000, 4097, 3001, "bf16"))
+    # bf16: 16-byte groups are 8 elements
+    bpads = lambda M, K, N, layout=0: {c for c in ext.hip_configs(M, K, N, "bf16", layout) if c[0].endswith("_pad")}
+    assert bpads(1000, 4097, 3001) and bpads(1024, 1024, 1020) and not pads(1024, 1024, 1020)
+    assert not bpads(1024, 1024, 1024) and not bpads(8192, 8192, 8192) and not bpads(1024, 1020, 1024, _lib.X1_COL_MAJOR)
+    assert ext.needs_pad(1024, 1020, 1024, 0, "bf16") and not ext.needs_pad(1024, 1020, 1024, 0, "f32")
     # layout: a column-major x1 is contiguous along M, a column-major x2 along K
     assert ext.needs_pad(1001, 1024, 1024, _lib.X1_COL_MAJOR) and not ext.needs_pad(1001, 1024, 1024)
     assert ext.needs_pad(1024, 1024, 1001) and not ext.needs_pad(1024, 1024, 1001, _lib.X2_COL_MAJOR)
@@ -471,6 +510,13 @@ def test_pad_variants_offered_for_unaligned_rows_and_sized():
     assert rc == _lib.OK and (ws, cnt) == (copies, 0)
     tiles = 8 * 24
     rc, ws, cnt = _scratch(M, N, K, 0, 0, 0, variant=vid, split=4)
+    assert rc == _lib.OK and ws == copies + 4 * tiles * 128 * 128 * 4 and cnt == tiles * 64 * 4
+    vid = _lib.variant_id("gemm_bf16_128x128x64_r4_m16_pad")
+    kp, m8, n8 = 4160, 1000, 3008
+    copies = -(-m8 * kp * 2 // 256) * 256 + -(-n8 * kp * 2 // 256) * 256
+    rc, ws, cnt = _scratch(M, N, K, 0, 0, 0, dtype=_lib.BF16, variant=vid, split=1)
+    assert rc == _lib.OK and (ws, cnt) == (copies, 0)
+    rc, ws, cnt = _scratch(M, N, K, 0, 0, 0, dtype=_lib.BF16, variant=vid, split=4)
     assert rc == _lib.OK and ws == copies + 4 * tiles * 128 * 128 * 4 and cnt == tiles * 64 * 4
 
 

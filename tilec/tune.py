@@ -60,15 +60,31 @@ LAUNCH_S = 3e-6        # a launch's fixed cost on MI355X (the 1x1x1 product's de
 COMBINE_S = 1.5e-6     # a split-K count-and-combine after the last row
 
 
-def roofline(M, K, N, cus, dtype, kernel, split_k):
+def prepass(M, K, N, dtype, kernel, layout=0):
+    """(launches, bytes moved) of the copies a variant makes before its GEMM:
+    the transposing variants (`*_kc`) transpose each operand that is not
+    k-contiguous (none when M, N or K is not a multiple of 8: the plain tile
+    runs), the pad variants (`*_pad`) copy both operands."""
+    esz = 4 if dtype == "f32" else 2
+    if kernel.endswith("_pad"):
+        return 2, 2 * esz * (M * K + K * N)
+    if kernel.endswith("_kc") and M % 8 == 0 and N % 8 == 0 and K % 8 == 0:
+        t1, t2 = bool(layout & _lib.X1_COL_MAJOR), not layout & _lib.X2_COL_MAJOR
+        if t1 or t2:
+            return int(t1) + int(t2), 2 * esz * (M * K * t1 + K * N * t2)
+    return 0, 0
+
+
+def roofline(M, K, N, cus, dtype, kernel, split_k, layout=0):
     """Analytic estimate for one (shape, config), the terms the trees cannot
     derive from sizes alone: the time at the matrix peak scaled by the share
     of CUs the grid fills and by the tile padding, the algorithmic HBM bytes
     (plus split-K partials written and read back), the operand re-reads of
-    the tile grid, a launch and a combine; also the padding efficiency, the
-    fill of the last round of workgroups and the K rows each wave takes.
-    Returns (t_est, t_compute, t_hbm, t_reread, pad, tail, fill, k_per_wave,
-    rounds)."""
+    the tile grid, a launch and a combine, and any copies of the operands
+    before the GEMM (`prepass`: a launch each, their bytes at half the HBM
+    rate); also the padding efficiency, the fill of the last round of
+    workgroups and the K rows each wave takes.  Returns (t_est, t_compute,
+    t_hbm, t_reread, pad, tail, fill, k_per_wave, rounds)."""
     v = _variant_by_name()[kernel]
     esz = 4 if dtype == "f32" else 2
     bm, bn = v["bm"], v["bn"]
@@ -82,7 +98,9 @@ def roofline(M, K, N, cus, dtype, kernel, split_k):
     t_c = 2.0 * M * N * K / (PEAK_FLOPS[dtype] * max(fill * pad, 1e-9))
     t_m = (esz * (M * K + K * N) + 4 * M * N + (8.0 * tiles * bm * bn * split_k if split_k > 1 else 0)) / PEAK_HBM
     t_r = esz * (M * K * cdiv(N, bn) + K * N * cdiv(M, bm)) / PEAK_L2_READ
-    t_est = max(t_c, t_m, t_r) + LAUNCH_S + (COMBINE_S if split_k > 1 else 0)
+    launches, moved = prepass(M, K, N, dtype, kernel, layout)
+    t_est = (max(t_c, t_m, t_r) + LAUNCH_S * (1 + launches) + 2.0 * moved / PEAK_HBM +
+             (COMBINE_S if split_k > 1 else 0))
     return t_est, t_c, t_m, t_r, pad, tail, fill, max(1.0, K / split_k / v["waves"]), float(rounds)
 
 
@@ -99,12 +117,19 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
     row-tile kernels take only such operands and run a slower fallback of
     the same tile for the others, a difference the sizes alone do not show
     the trees (on MI355X it took the held-out worst case from 2.3x to 1.5x).
+    Then three variant properties the descriptor sizes do not carry: 16x16
+    MFMA blocks (`*_m16`), operands transposed (`*_kc`) or padded (`*_pad`)
+    into the workspace first — otherwise such a variant and its plain
+    counterpart look the same to the trees.  Last, whether this config runs
+    a slower fallback of its tile for these operands (`falls_back`): the
+    alignment bits alone describe the shape, and the trees then have to
+    learn which variants they matter for.
     """
     v = _variant_by_name()[kernel]
     tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
     wgs = tiles * split_k
     lg = lambda x: math.log2(max(1, x))
-    t_est, t_c, t_m, t_r, pad, tail, fill, kpw, rounds = roofline(M, K, N, cus, dtype, kernel, split_k)
+    t_est, t_c, t_m, t_r, pad, tail, fill, kpw, rounds = roofline(M, K, N, cus, dtype, kernel, split_k, layout)
     ls = lambda t: math.log2(max(t, 1e-12))
     return [lg(M), lg(K), lg(N), cus, 1.0 if dtype == "bf16" else 0.0,
             float(v["family"]), lg(v["bm"]), lg(v["bn"]), lg(v["bk"]), float(v["waves"]),
@@ -114,7 +139,27 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
             float(v["max_m"]),
             ls(t_est), ls(t_c), ls(t_m), ls(t_r), pad, tail, fill, lg(kpw), rounds,
             float(aligned(M if layout & _lib.X1_COL_MAJOR else K, dtype)),
-            float(aligned(K if layout & _lib.X2_COL_MAJOR else N, dtype))]
+            float(aligned(K if layout & _lib.X2_COL_MAJOR else N, dtype)),
+            float("_m16" in kernel), float(kernel.endswith("_kc")), float(kernel.endswith("_pad")),
+            float(falls_back(kernel, M, K, N, dtype, layout))]
+
+
+def falls_back(kernel, M, K, N, dtype, layout=0):
+    """Whether a tile-GEMM variant runs a slower fallback of its tile for
+    these operands: the direct-to-LDS tiles (fp32 `*_lds`, the bf16 tiles
+    with a ring of stage buffers) take only operands whose contiguous extents
+    are whole 16-byte groups.  The bf16 transposing variants (`*_kc`) copy
+    operands whose M, N and K are multiples of 8 into that form and run the
+    plain tile on the others.  The pad variants exist for the other shapes
+    and never fall back."""
+    v = _variant_by_name()[kernel]
+    if v["family"] != _lib.FAMILY_GEMM or kernel.endswith("_pad"):
+        return False
+    if kernel.endswith("_kc") and M % 8 == 0 and N % 8 == 0 and K % 8 == 0:
+        return False
+    lds = kernel.endswith("_lds") if dtype == "f32" else v["unroll"] >= 2
+    return lds and not (aligned(M if layout & _lib.X1_COL_MAJOR else K, dtype) and
+                        aligned(K if layout & _lib.X2_COL_MAJOR else N, dtype))
 
 
 def aligned(extent, dtype):
@@ -315,15 +360,33 @@ def _narrow_stream(rng, count):
     return got
 
 
-def shapes(n=500, seed=0, n_layout=120, n_rows=40, n_tile=30, n_medium=80, n_narrow=60):
+def _bf16_stream(rng, count):
+    """bf16 tile GEMMs in every layout: M in [64, 8192], K in [256, 8192],
+    N in [64, 8192] log-uniform — the regime with the most variants (two
+    MFMA forms, prep and split choices), where held-out picks of models
+    trained without this stream erred most."""
+    got = set()
+    while len(got) < count:
+        M = round(2 ** rng.uniform(6, 13))
+        K = round(2 ** rng.uniform(8, 13))
+        N = round(2 ** rng.uniform(6, 13))
+        if rng.random() < 0.5:
+            K = 1 << round(math.log2(K))
+        if M * K * N <= 1 << 33 and M * K <= 1 << 26 and K * N <= 1 << 26:
+            got.add((M, K, N, "bf16", rng.choice((0, 1, 2, 3))))
+    return got
+
+
+def shapes(n=500, seed=0, n_layout=120, n_rows=40, n_tile=30, n_medium=80, n_narrow=60, n_bf16=80):
     """Seeded random shapes (M, K, N, dtype, layout): `n` row-major draws plus
     CONFIG_SHAPES, `n_layout` draws of a second stream (seed + 1) with a
     random non-row-major layout, plus LAYOUT_CONFIG_SHAPES, `n_rows` x @ W.T
     shapes with M <= 4 from a third stream (seed + 2), the row-dot kernel's
     domain, `n_tile` x @ W.T shapes with 5 <= M <= 16 from a fourth
-    (seed + 3), the row-tile kernel's, and row-major `n_medium` medium
+    (seed + 3), the row-tile kernel's, row-major `n_medium` medium
     outputs (seed + 4) and `n_narrow` narrow outputs over a long K
-    (seed + 5).  None of UNSEEN_SHAPES is ever included."""
+    (seed + 5), and `n_bf16` bf16 tile GEMMs in random layouts (seed + 6).
+    None of UNSEEN_SHAPES is ever included."""
     rng = random.Random(seed)
     out = set(CONFIG_SHAPES)
     while len(out) < n + len(CONFIG_SHAPES):
@@ -352,6 +415,7 @@ def shapes(n=500, seed=0, n_layout=120, n_rows=40, n_tile=30, n_medium=80, n_nar
     tile = wt_stream(random.Random(seed + 3), n_tile, 5, 16)
     more = {t + (0,) for t in _medium_stream(random.Random(seed + 4), n_medium) |
             _narrow_stream(random.Random(seed + 5), n_narrow)}
+    more |= _bf16_stream(random.Random(seed + 6), n_bf16)
     unseen = {u + (0,) for u in UNSEEN_SHAPES}
     return sorted((out | lay | rows | tile | more) - unseen, key=lambda s: (s[0] * s[1] * s[2], s))
 
@@ -489,7 +553,6 @@ def train(test_frac=0.2, seeds=(0, 1, 2), out=MODEL, path=None):
     library's built-in rule over several random 80/20 splits of the shapes
     (one per seed: the worst case of one split moves with the split); refit
     on everything and export JSON (tilec/tune.py:99-132)."""
-    from sklearn.ensemble import GradientBoostingRegressor
     from . import ext
     rows = load(path)
     names = _variant_by_name()
@@ -500,27 +563,27 @@ def train(test_frac=0.2, seeds=(0, 1, 2), out=MODEL, path=None):
              (r["kernel"], int(r["split_k"])) in ext.hip_configs(*_key(r)[:4], int(r["layout"])))]
     feats = {id(r): row_features(r) for r in rows}
 
-    def fit(rs, seed):
-        X = [feats[id(r)] for r in rs]
-        y = [math.log(max(r["ms"], 1e-6)) for r in rs]
-        # The reference's GBR(300, lr 0.05) with trees of depth 6 instead of 4:
-        # on this data set (three 80/20 shape splits) depth 6 ran the held-out
-        # picks 1.063x of the best config (geomean) against 1.112x with
-        # depth 4; depth 8 overfits (worst 10x).
-        return GradientBoostingRegressor(n_estimators=300, max_depth=6, learning_rate=0.05,
-                                         random_state=seed).fit(X, y)
+    def data(rs):
+        return [feats[id(r)] for r in rs], [math.log(max(r["ms"], 1e-6)) for r in rs]
 
     by_shape = {}
     for r in rows:
         by_shape.setdefault(_key(r), []).append(r)
-    L = _lib.lib()
-    gm = lambda v: math.exp(sum(math.log(a) for a in v) / len(v)) if v else float("nan")
-    splits = []
+    tests = []
     for seed in seeds:
         keys = sorted(by_shape)
         random.Random(seed).shuffle(keys)
-        test = set(keys[:int(len(keys) * test_frac)])
-        model = fit([r for r in rows if _key(r) not in test], seed)
+        tests.append(set(keys[:int(len(keys) * test_frac)]))
+    # one fit per held-out split and one on everything, in parallel processes
+    jobs = [data([r for r in rows if _key(r) not in test]) + (seed,) for seed, test in zip(seeds, tests)]
+    jobs.append(data(rows) + (seeds[0],))
+    import multiprocessing
+    with multiprocessing.get_context("fork").Pool(min(len(jobs), os.cpu_count() or 1)) as pool:
+        models = pool.map(_fit_gbr, jobs)
+    L = _lib.lib()
+    gm = lambda v: math.exp(sum(math.log(a) for a in v) / len(v)) if v else float("nan")
+    splits = []
+    for seed, test, model in zip(seeds, tests, models):
         ratio_model, ratio_default, worst = [], [], None
         for k in sorted(test):
             rs = by_shape[k]
@@ -556,9 +619,18 @@ def train(test_frac=0.2, seeds=(0, 1, 2), out=MODEL, path=None):
     print(f"over {len(splits)} splits: model {report['model_geomean_vs_best']:.3f}x (geo mean of geo means), "
           f"worst {report['model_worst_vs_best']:.2f}x; builtin {report['builtin_geomean_vs_best']:.3f}x, "
           f"worst {report['builtin_worst_vs_best']:.2f}x")
-    model = fit(rows, seeds[0])
-    export(model, out, report, best_table(rows))
+    export(models[-1], out, report, best_table(rows))
     return report
+
+
+def _fit_gbr(job):
+    """GBR on (X, y, seed).  The reference's GBR(300, lr 0.05) with trees of
+    depth 6 instead of 4: on this data set (three 80/20 shape splits) depth 6
+    ran the held-out picks 1.063x of the best config (geomean) against 1.112x
+    with depth 4; depth 8 overfits (worst 10x)."""
+    from sklearn.ensemble import GradientBoostingRegressor
+    X, y, seed = job
+    return GradientBoostingRegressor(n_estimators=300, max_depth=6, learning_rate=0.05, random_state=seed).fit(X, y)
 
 
 def best_table(rows):
