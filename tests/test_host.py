@@ -166,16 +166,19 @@ def test_gemm_split_geometry_matches_the_library():
 
 def test_row_dot_configs_only_where_the_kernel_runs():
     """The x @ W.T variants (row-dot, M <= 4; row-tile, M <= 16) are offered
-    unsplit, for x2 column-major and K a multiple of the 16-byte group;
-    elsewhere they would run the streaming kernel unsplit."""
+    unsplit, for x2 column-major, the row-tile kernel only for K a multiple
+    of the 16-byte group (the row-dot kernel takes any K); elsewhere they
+    would run the streaming kernel unsplit."""
     rows = lambda cfgs: [c for c in cfgs if ext.rows_variant(_lib.variants()[_lib.variant_id(c[0])])]
     f32 = rows(ext.hip_configs(1, 4096, 4096, "f32", _lib.X2_COL_MAJOR))
     assert f32 and all(s == 1 for _, s in f32)
     assert rows(ext.hip_configs(4, 4096, 4096, "bf16", _lib.X2_COL_MAJOR))
     assert not rows(ext.hip_configs(1, 4096, 4096, "f32", 0))
     assert not rows(ext.hip_configs(1, 4096, 4096, "f32", _lib.X1_COL_MAJOR | _lib.X2_COL_MAJOR))
-    assert not rows(ext.hip_configs(1, 4094, 4096, "f32", _lib.X2_COL_MAJOR))
-    assert not rows(ext.hip_configs(1, 4092, 4096, "bf16", _lib.X2_COL_MAJOR))
+    odd = rows(ext.hip_configs(1, 4094, 4096, "f32", _lib.X2_COL_MAJOR))
+    assert odd and not any(c.endswith(("_c128", "_c256")) for c, _ in odd)
+    assert rows(ext.hip_configs(4, 4092, 4096, "bf16", _lib.X2_COL_MAJOR))
+    assert not rows(ext.hip_configs(5, 4092, 4096, "bf16", _lib.X2_COL_MAJOR))  # row-tile only, K % 8
     m5 = rows(ext.hip_configs(5, 4096, 4096, "f32", _lib.X2_COL_MAJOR))
     assert m5 and all(c.endswith(("_c128", "_c256")) for c, _ in m5)  # only the row-tile kernel above M = 4
     assert rows(ext.hip_configs(16, 4096, 4096, "bf16", _lib.X2_COL_MAJOR))
@@ -592,8 +595,10 @@ def test_select_variant_rules():
     assert names[L.tilec_select_variant_layout(1, 4096, 4096, 0, wt, 0, 0)] == "skinny_f32_t1_r1_w8_u2"
     assert names[L.tilec_select_variant_layout(16, 4096, 4096, 1, wt, 0, 0)] == "skinny_bf16_t16_r16_w8_c128"
     assert L.tilec_select_variant_layout(1, 4096, 4096, 0, 0, 0, 0) == L.tilec_select_variant(1, 4096, 4096, 0)
-    # an unaligned stride: the row-dot kernel does not take it
-    assert not names[L.tilec_select_variant_layout(1, 4096, 4097, 0, wt, 0, 4099)].startswith("skinny_f32_t1")
+    # unaligned K or strides: the row-dot kernel takes them, the row-tile kernel does not
+    assert names[L.tilec_select_variant_layout(1, 4096, 4097, 0, wt, 0, 4099)] == "skinny_f32_t1_r1_w8_u2"
+    assert names[L.tilec_select_variant_layout(1, 4096, 4095, 1, wt, 4095, 4095)] == "skinny_bf16_t1_r1_w8_u2"
+    assert not names[L.tilec_select_variant_layout(8, 4096, 4097, 0, wt, 0, 4099)].endswith("_c128")
     assert L.tilec_select_variant_layout(4, 4, 4, 0, 8, 0, 0) == -_lib.ERR_VALUE
 
 

@@ -714,6 +714,48 @@ def test_pad_variants_any_alignment():
                         np.testing.assert_array_equal(got, want)
 
 
+def test_row_dot_any_alignment():
+    """The row-dot kernel (x @ W.T, M <= 4) at every element misalignment of
+    K, of both row strides and of both bases: its own kernel runs (no
+    scratch) and matches the fp64 oracle, and small integers exactly.  Past
+    K a row's last 16-byte chunk holds the row stride's padding, NaN here,
+    which must not leak in."""
+    rows = [v for v in _lib.variants() if ext.rows_variant(v) and not v["name"].endswith(("_c128", "_c256"))]
+    assert len(rows) == 8
+    shapes = [(1, 1001, 37), (4, 517, 300), (3, 4099, 64), (1, 3, 9), (2, 2053, 129)]
+    for i, (m, k, n) in enumerate(shapes):
+        a, b = O.normal((m, k), 1500 + 2 * i), O.normal((k, n), 1501 + 2 * i)
+        ai, bi = O.small_ints((m, k), 1520 + 2 * i, -3, 3), O.small_ints((k, n), 1521 + 2 * i, -3, 3)
+        want = (ai.astype(np.int64) @ bi.astype(np.int64)).astype(np.float32)
+        for v in rows:
+            if m > v["max_m"]:
+                continue
+            bf16 = v["dtype"] == _lib.BF16
+            if bf16:
+                a16, b16 = O.bf16_round(a), O.bf16_round(b)
+                x1, x2, ref, tol = dev_bf16(a16), dev_bf16(b16), O.matmul_bf16_f64(a16, b16), 1e-5
+                y1, y2 = dev(ai, torch.bfloat16), dev(bi, torch.bfloat16)
+            else:
+                x1, x2, ref, tol = dev(a), dev(b), O.matmul_f64(a, b), O.TOL_F32
+                y1, y2 = dev(ai), dev(bi)
+            for off, extra in ((0, 0), (1, 3), (3, 1), (5, 2)):
+                say(f"{v['name']} offset {off} extra {extra} shape {(m, k, n)}")
+                views = []
+                for p1, p2 in ((x1, x2), (y1, y2)):
+                    v1 = _view_at(p1, False, off, extra)
+                    v2 = _view_at(p2, True, off + 2, extra)
+                    # the padding between rows of x1 and of W (and past the last) is NaN
+                    if extra:
+                        v1.as_strided((m, extra), (k + extra, 1), v1.storage_offset() + k).fill_(float("nan"))
+                        v2.as_strided((n, extra), (k + extra, 1), v2.storage_offset() + k).fill_(float("nan"))
+                    views.append((v1, v2))
+                wv = views[0][1]
+                assert ext.layout_of(views[0][0], wv) == _lib.X2_COL_MAJOR
+                got = run(*views[0], (v["name"], 1))
+                assert O.rel_l2(got, ref) <= tol, (v["name"], off, extra, (m, k, n))
+                np.testing.assert_array_equal(run(*views[1], (v["name"], 1)), want)
+
+
 def test_layouts_padded_strides_and_splits():
     """Column strides above the row count, and K splits of the tile GEMMs,
     in every layout."""

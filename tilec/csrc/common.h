@@ -391,6 +391,30 @@ __device__ __forceinline__ void tile_of(int bid, int xcds, int tiles_m, int tile
 // ---------------------------------------------------------------------------
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Bytes [b, b + 16) of the 32 bytes lo:hi (b < 16): v_alignbyte over the
+// window of dwords that starts at dword b / 4.
+__device__ __forceinline__ u32x4 funnel16(u32x4 lo, u32x4 hi, uint32_t b) {
+  const uint32_t d[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  const uint32_t w = b >> 2, rb = b & 3;
+  uint32_t e[5];
+#pragma unroll
+  for (int j = 0; j < 5; ++j) e[j] = w == 0 ? d[j] : w == 1 ? d[j + 1] : w == 2 ? d[j + 2] : d[j + 3];
+  u32x4 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = __builtin_amdgcn_alignbyte(e[j + 1], e[j], rb);
+  return v;
+}
+
+// v with its bytes from `keep` on cleared (keep <= 0: all of them).
+__device__ __forceinline__ u32x4 keep_bytes(u32x4 v, int keep) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int kb = keep - 4 * j;
+    v[j] = kb >= 4 ? v[j] : kb <= 0 ? 0u : (v[j] & ((1u << (8 * kb)) - 1u));
+  }
+  return v;
+}
+
 template <int ESZ>
 __global__ __launch_bounds__(256) void pad_copy_kernel(const unsigned char* __restrict__ in,
                                                        unsigned char* __restrict__ out, int64_t R, int64_t C,
@@ -410,21 +434,8 @@ __global__ __launch_bounds__(256) void pad_copy_kernel(const unsigned char* __re
       const u32x4 a0 = *reinterpret_cast<const u32x4*>(lo);
       u32x4 a1 = {0u, 0u, 0u, 0u};
       if (b != 0 && c0 * ESZ + 16 < (int64_t)b + C * ESZ) a1 = *reinterpret_cast<const u32x4*>(lo + 16);
-      const uint32_t d[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      const uint32_t w = b >> 2, rb = b & 3;
-      uint32_t e[5];
-#pragma unroll
-      for (int j = 0; j < 5; ++j) e[j] = w == 0 ? d[j] : w == 1 ? d[j + 1] : w == 2 ? d[j + 2] : d[j + 3];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = __builtin_amdgcn_alignbyte(e[j + 1], e[j], rb);
-      if (c0 + EPC > C) {  // the row's last chunk: zero the elements past C
-        const int keep = (int)(C - c0) * ESZ;  // bytes kept
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int kb = keep - 4 * j;
-          v[j] = kb >= 4 ? v[j] : kb <= 0 ? 0u : (v[j] & ((1u << (8 * kb)) - 1u));
-        }
-      }
+      v = funnel16(a0, a1, b);
+      if (c0 + EPC > C) v = keep_bytes(v, (int)(C - c0) * ESZ);  // the row's last chunk: zero past C
     }
     *reinterpret_cast<u32x4*>(out + (r * Cp + c0) * ESZ) = v;
   }

@@ -619,8 +619,16 @@ hipError_t launch_skinny(const MatmulArgs& a) {
 // masked by the buffer resources' extents (one resource per row, num_records
 // = K elements): they load zeros.  W is read with the non-temporal cache
 // policy CP (streamed once); x1 stays cached.  No LDS, no barriers.
+//
+// AL: every row starts on a 16-byte boundary (K, both strides and both
+// bases aligned).  Otherwise (any element alignment) each row's resource
+// starts at the 16-byte boundary below the row and ends at the one above
+// its last element, a lane loads the two aligned chunks its 16 bytes span
+// and shifts them into place by the row's byte misalignment (funnel16), and
+// elements past K, which now share a chunk with the next row, are cleared
+// in both operands.  No load leaves the row's own 16-byte chunks.
 // ---------------------------------------------------------------------------
-template <typename T, int MR, int RPW, int WAVES, int U, int CP>
+template <typename T, int MR, int RPW, int WAVES, int U, int CP, bool AL>
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restrict__ x1, const T* __restrict__ w,
                                                                float* __restrict__ out, int M, int N, int K,
                                                                int64_t ldx1, int64_t ldw, int64_t ldo) {
@@ -633,10 +641,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
   if (row0 >= N) return;
   const uint32_t kbytes = (uint32_t)K * sizeof(T);
   BufRsrc rw[RPW], rx[MR];
+  uint32_t bw[RPW], bx[MR];  // byte misalignment of each row (AL: 0)
+  auto row_rsrc = [&](const T* p, bool ok, uint32_t& b) -> BufRsrc {
+    if constexpr (AL) {
+      b = 0;
+      return make_rsrc(p, ok ? kbytes : 0u);
+    } else {
+      const uintptr_t s = reinterpret_cast<uintptr_t>(p);
+      b = (uint32_t)(s & 15);
+      return make_rsrc(reinterpret_cast<const void*>(s - b), ok ? (b + kbytes + 15u) & ~15u : 0u);
+    }
+  };
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) rw[r] = make_rsrc(w + (int64_t)(row0 + r) * ldw, row0 + r < N ? kbytes : 0u);
+  for (int r = 0; r < RPW; ++r) rw[r] = row_rsrc(w + (int64_t)(row0 + r) * ldw, row0 + r < N, bw[r]);
 #pragma unroll
-  for (int m = 0; m < MR; ++m) rx[m] = make_rsrc(x1 + (int64_t)m * ldx1, m < M ? kbytes : 0u);
+  for (int m = 0; m < MR; ++m) rx[m] = row_rsrc(x1 + (int64_t)m * ldx1, m < M, bx[m]);
   auto ld = [&](const BufRsrc& rs, uint32_t off) -> V {
     return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
   };
@@ -647,8 +666,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
     if constexpr (sizeof(T) == 4) return v[e];
     else return (e & 1) ? bf16_hi(v[e >> 1]) : bf16_lo(v[e >> 1]);
   };
+  constexpr int NH = AL ? 1 : 2;  // aligned chunks loaded per 16 bytes used
   struct Batch {
-    V w[U][RPW], x[U][MR];
+    V w[U][RPW][NH], x[U][MR][NH];
   };
   float acc[RPW][MR];
 #pragma unroll
@@ -662,22 +682,42 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
       // chunk c0 + u; past K every element is masked (offset >= extent)
       const uint32_t off = (uint32_t)(c0 + u) * (uint32_t)CH * sizeof(T) + lane_off;
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) b.w[u][r] = ld_w(rw[r], off);
+      for (int h = 0; h < NH; ++h) {
 #pragma unroll
-      for (int m = 0; m < MR; ++m) b.x[u][m] = ld(rx[m], off);
+        for (int r = 0; r < RPW; ++r) b.w[u][r][h] = ld_w(rw[r], off + 16u * h);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) b.x[u][m][h] = ld(rx[m], off + 16u * h);
+      }
     }
   };
-  auto fma = [&](const Batch& b) __attribute__((always_inline)) {
+  // The 16 bytes a lane uses (AL: as loaded).
+  auto use = [&](const V (&v)[NH], uint32_t b, int kvalid) -> V {
+    if constexpr (AL) {
+      return v[0];
+    } else {
+      u32x4 x = funnel16(__builtin_bit_cast(u32x4, v[0]), __builtin_bit_cast(u32x4, v[NH - 1]), b);
+      if (kvalid < EPL) x = keep_bytes(x, kvalid * (int)sizeof(T));
+      return __builtin_bit_cast(V, x);
+    }
+  };
+  auto fma = [&](int c0, const Batch& b) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
+      const int kvalid = K - (c0 + u) * CH - EPL * lane;  // elements of this lane's 16 bytes inside K
+      V wv[RPW], xv[MR];
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) wv[r] = use(b.w[u][r], bw[r], kvalid);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) xv[m] = use(b.x[u][m], bx[m], kvalid);
 #pragma unroll
       for (int e = 0; e < EPL; ++e)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          const float xv = elem(b.x[u][m], e);
+          const float xe = elem(xv[m], e);
 #pragma unroll
-          for (int r = 0; r < RPW; ++r) acc[r][m] = __builtin_fmaf(elem(b.w[u][r], e), xv, acc[r][m]);
+          for (int r = 0; r < RPW; ++r) acc[r][m] = __builtin_fmaf(elem(wv[r], e), xe, acc[r][m]);
         }
+    }
   };
   const int nch = (K + CH - 1) / CH;
   const int nb = (nch + U - 1) / U;
@@ -686,14 +726,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
   for (int i = 0; i + 1 < nb; i += 2) {
     load((i + 1) * U, B);
     __builtin_amdgcn_sched_barrier(0);
-    fma(A);
+    fma(i * U, A);
     __builtin_amdgcn_sched_barrier(0);
     load((i + 2) * U, A);
     __builtin_amdgcn_sched_barrier(0);
-    fma(B);
+    fma((i + 1) * U, B);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (nb & 1) fma(A);
+  if (nb & 1) fma((nb - 1) * U, A);
   // Butterfly over the 64 lanes; every lane ends with the full sums.
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
@@ -850,25 +890,32 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
   }
 }
 
-// x @ W.T with a 16-byte aligned row-major x1 and W (K and both strides
-// multiples of the 16-byte element count), M <= MR: the row-dot kernel; any
-// other layout or alignment runs the streaming kernel's variant FB.
+// x @ W.T with a row-major x1 and W, M <= MR: the row-dot kernel, at any
+// element alignment of K, strides and bases; any other layout runs the
+// streaming kernel's variant FB.
 template <typename T, int MR>
 bool rows_fit(const MatmulArgs& a) {
+  return (a.layout & 3) == TILEC_X2_COL_MAJOR && a.M <= MR &&
+         (int64_t)a.K * (int64_t)sizeof(T) < (int64_t(1) << 31) - 64;
+}
+
+// Every row of x1 and W starts on a 16-byte boundary.
+template <typename T>
+bool rows_aligned(const MatmulArgs& a) {
   constexpr int EPL = 16 / (int)sizeof(T);
   auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  return (a.layout & 3) == TILEC_X2_COL_MAJOR && a.M <= MR && a.K % EPL == 0 && a.ldx1 % EPL == 0 &&
-         a.ldx2 % EPL == 0 && aligned(a.x1) && aligned(a.x2) &&
-         (int64_t)a.K * (int64_t)sizeof(T) < (int64_t(1) << 31) - 64;
+  return a.K % EPL == 0 && a.ldx1 % EPL == 0 && a.ldx2 % EPL == 0 && aligned(a.x1) && aligned(a.x2);
 }
 
 template <typename T, int MR, int RPW, int WAVES, int U, int CP, typename FB>
 hipError_t launch_rows(const MatmulArgs& a, FB fallback) {
   if (!rows_fit<T, MR>(a)) return fallback(a);
   const int64_t rows_per_wg = (int64_t)WAVES * RPW;
-  hipLaunchKernelGGL((gemv_rows_kernel<T, MR, RPW, WAVES, U, CP>), dim3((unsigned)cdiv(a.N, rows_per_wg)), dim3(WAVES * 64),
-                     0, a.stream, static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out, (int)a.M, (int)a.N,
-                     (int)a.K, a.ldx1, a.ldx2, a.ldo);
+  auto kern = rows_aligned<T>(a) ? gemv_rows_kernel<T, MR, RPW, WAVES, U, CP, true>
+                                 : gemv_rows_kernel<T, MR, RPW, WAVES, U, CP, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(a.N, rows_per_wg)), dim3(WAVES * 64), 0, a.stream,
+                     static_cast<const T*>(a.x1), static_cast<const T*>(a.x2), a.out, (int)a.M, (int)a.N, (int)a.K,
+                     a.ldx1, a.ldx2, a.ldo);
   return hipGetLastError();
 }
 

@@ -152,9 +152,12 @@ int auto_variant(int64_t M, int64_t N, int64_t K, int dtype, int64_t ldx1, int64
   // variant chosen below for the same shape in another layout, so sizes
   // queried with TILEC_VARIANT_AUTO still suffice.
   const int64_t epl = dtype == TILEC_F32 ? 4 : 8;  // elements per 16-byte load
-  if ((layout & 3) == TILEC_X2_COL_MAJOR && M >= 1 && M <= 16 && K % epl == 0 && ldx1 % epl == 0 &&
+  // (the row-dot kernel takes any element alignment, the row-tile kernel
+  // whole 16-byte rows)
+  if ((layout & 3) == TILEC_X2_COL_MAJOR && M == 1 && skinny_fits(ldx1, ldx2, layout))
+    return find(dtype == TILEC_F32 ? "skinny_f32_t1_r1_w8_u2" : "skinny_bf16_t1_r1_w8_u2");
+  if ((layout & 3) == TILEC_X2_COL_MAJOR && M >= 2 && M <= 16 && K % epl == 0 && ldx1 % epl == 0 &&
       ldx2 % epl == 0 && skinny_fits(ldx1, ldx2, layout)) {
-    if (M == 1) return find(dtype == TILEC_F32 ? "skinny_f32_t1_r1_w8_u2" : "skinny_bf16_t1_r1_w8_u2");
     // one workgroup per 16 rows of W: with fewer than half the CUs busy
     // and a long K, the streaming kernel's K split (below) is faster
     if (cdiv(N, 16) >= cus / 2 || K <= 2048)

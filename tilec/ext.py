@@ -79,10 +79,11 @@ _SKINNY_SPLITS = (1, 2, 4, 8, 16, 32, 64)
 def hip_configs(M, K, N, dtype="f32", layout=None):
     """Every (variant, split_k) the library can run for out[M,N] = x1[M,K]·x2[K,N].
 
-    The row-dot variants are offered only where their kernel runs: K a
-    multiple of the 16-byte element count and, with `layout` given, x @ W.T
-    (x2 column-major, x1 row-major).  Elsewhere they run the streaming
-    kernel unsplit, which is never the config to pick.
+    The row-dot and row-tile variants are offered only where their kernel
+    runs: with `layout` given, x @ W.T (x2 column-major, x1 row-major), and
+    for the row-tile kernel K a multiple of the 16-byte element count (the
+    row-dot kernel takes any K).  Elsewhere they run the streaming kernel
+    unsplit, which is never the config to pick.
 
     The skinny family (a K split, 16-row blocks) and the direct family (fp32
     MFMAs on operands loaded straight into registers, a K split) are offered
@@ -107,8 +108,9 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             continue  # aligned operands: the direct-to-LDS variants read them in place
         if v["family"] == _lib.FAMILY_SKINNY and rows_variant(v):
             epl = 4 if code == _lib.F32 else 8  # elements per 16-byte load
-            if K % epl == 0 and (layout is None or layout == _lib.X2_COL_MAJOR):
-                out.append((v["name"], 1))  # the row-dot kernel never splits K
+            row_tile = v["name"].endswith(("_c128", "_c256"))  # the row-dot kernel takes any K
+            if (K % epl == 0 or not row_tile) and (layout is None or layout == _lib.X2_COL_MAJOR):
+                out.append((v["name"], 1))  # neither kernel splits K
         elif v["family"] == _lib.FAMILY_DIRECT:
             # Any split that leaves every wave at least one 16-row step;
             # no tile more than twice as tall as M needs.
