@@ -22,6 +22,9 @@ and W warmup steps.  Extra objects in the same line:
   layouts      — transposed operands read in place: x @ W.T GEMV (weight
                  W [N, K] row-major) as in `skinny`, and the 4096^3 fp32 /
                  8192^3 bf16 GEMMs with x1, x2 or both column-major
+  ragged_bf16  — bf16 products whose operand rows are not whole 16-byte
+                 groups: the library's pick (a pad variant) beside the plain
+                 variant of the same tile and torch.mm, graph-replayed
   reduce       — row and column sums (ext.sum, the reference's tl.sum) in
                  HBM GB/s, graph-replayed over rotating inputs, beside
                  torch.sum of the same inputs timed the same way
@@ -70,7 +73,7 @@ def parse():
                    help="with --only skinny, configs or reduce: run only the cases whose key contains this "
                         "text (one kernel per profile run)")
     p.add_argument("--only", choices=["square", "skinny", "bf16", "configs", "layouts", "reduce", "vendor", "copy",
-                                      "host", "tuner", "cpu", "ksweep", "floor"],
+                                      "host", "tuner", "cpu", "ksweep", "floor", "ragged_bf16"],
                    help="run one section and print its own JSON (for profiling); 'copy' is a plain "
                         "device copy of 256 MiB, the calibration run for the FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
@@ -427,6 +430,50 @@ def bench_configs(reps=20):
     return out
 
 
+RAGGED_BF16_CASES = (
+    # (name, M, K, N, layout): bf16 products whose operand rows are not whole
+    # 16-byte groups (the pad variants' domain), from the tuner's data, and a
+    # square one just short of 8192^3
+    ("bf16_1359x4447x1009", 1359, 4447, 1009, 0),
+    ("bf16_4354x4096x330_x1T", 4354, 4096, 330, 1),
+    ("bf16_560x4565x3046_x1T_x2T", 560, 4565, 3046, 3),
+    ("bf16_8191", 8191, 8191, 8191, 0),
+)
+
+
+def bench_ragged_bf16(reps=10):
+    """bf16 products with unaligned operand rows: device time per call of the
+    library's pick (a pad variant: both operands copied into the workspace
+    with 16-byte rows, then the LDS-DMA tile) from a HIP graph of `reps`
+    calls, beside the plain variant of the same tile on the operands as they
+    are (its register-staged fallback) and torch.mm (hipBLASLt), timed the
+    same way."""
+    import torch
+    from tilec import ext, tune
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for name, M, K, N, layout in RAGGED_BF16_CASES:
+        if CASE is not None and CASE not in name:
+            continue
+        x1, x2 = tune.operands(M, K, N, "bf16", layout, g)
+        cfg = tuple(tune.pick(M, K, N, "bf16", layout) or ("auto", 0))
+        n = max(2, min(reps, int(reps * 2e9 / (M * K * N))))
+        ms = _graph_ms(lambda: ext.matrix_mul(x1, x2), n)
+        rec = dict(us=ms * 1e3, TFLOPs=2 * M * N * K / (ms * 1e-3) / 1e12, layout=layout, config=list(cfg))
+        if cfg[0].endswith("_pad"):
+            plain = (cfg[0][:-4], cfg[1])
+            plain_ms = _graph_ms(lambda: ext.matrix_mul(x1, x2, plain), n)
+            rec.update(plain=list(plain), plain_us=plain_ms * 1e3)
+        vendor_ms = _graph_ms(lambda: torch.mm(x1, x2).float(), n)
+        rec.update(torch_mm_us=vendor_ms * 1e3, speedup_vs_torch_mm=vendor_ms / ms)
+        rec["frac"] = rec["TFLOPs"] / PEAK_BF16_MFMA
+        out[name] = rec
+        log(f"{name}: {ms * 1e3:.1f} us ({cfg})" + (f", plain {rec['plain_us']:.1f} us" if "plain_us" in rec else "")
+            + f"; torch.mm {vendor_ms * 1e3:.1f} us")
+        del x1, x2
+    return out
+
+
 REDUCE_CASES = (
     # (name, R, C, dtype, axis): the config-1 x2 summed both ways, a few long
     # rows (split columns) and a tall, narrow bf16 matrix (split rows)
@@ -737,7 +784,7 @@ def main():
         out = {"square": lambda: bench_square(args), "skinny": bench_skinny, "bf16": bench_bf16,
                "configs": bench_configs, "layouts": bench_layouts, "reduce": bench_reduce,
                "vendor": bench_vendor, "copy": bench_copy, "host": bench_host, "tuner": bench_tuner,
-               "ksweep": bench_ksweep, "floor": bench_floor,
+               "ksweep": bench_ksweep, "floor": bench_floor, "ragged_bf16": bench_ragged_bf16,
                "cpu": lambda: bench_cpu(args.cpu_seconds)}[args.only]()
         print(json.dumps({"section": args.only, **out}), flush=True)
         return
@@ -749,6 +796,7 @@ def main():
         extra["bf16_8192"] = bench_bf16()
         extra["configs"] = bench_configs()
         extra["layouts"] = bench_layouts()
+        extra["ragged_bf16"] = bench_ragged_bf16()
         extra["reduce"] = bench_reduce()
         extra["host_overhead"] = bench_host()
         extra["tuner_unseen"] = bench_tuner()
