@@ -415,43 +415,60 @@ __device__ __forceinline__ u32x4 keep_bytes(u32x4 v, int keep) {
   return v;
 }
 
+// One operand of a padding copy: in (R x C, row stride ld) -> out (Rp x Cp,
+// row stride Cp); rows of 2^lg threads.
+struct PadCopyOp {
+  const unsigned char* in;
+  unsigned char* out;
+  int64_t R, C, ld, Rp, Cp;
+  int lg;
+};
+
+// Both operands in one launch (grid z selects the operand): at the sizes
+// where the pad variants win, a second launch's fixed cost is a few per cent.
 template <int ESZ>
-__global__ __launch_bounds__(256) void pad_copy_kernel(const unsigned char* __restrict__ in,
-                                                       unsigned char* __restrict__ out, int64_t R, int64_t C,
-                                                       int64_t ld, int64_t Rp, int64_t Cp, int lg) {
+__global__ __launch_bounds__(256) void pad_copy_kernel(PadCopyOp o0, PadCopyOp o1) {
   constexpr int EPC = 16 / ESZ;  // elements per 16-byte chunk
-  const int64_t nch = Cp / EPC;
-  const int64_t ch = (int64_t)blockIdx.x * (1 << lg) + (threadIdx.x & ((1 << lg) - 1));
-  const int64_t rpb = 256 >> lg;  // rows per workgroup
+  const PadCopyOp& o = blockIdx.z ? o1 : o0;
+  const int64_t nch = o.Cp / EPC;
+  const int64_t ch = (int64_t)blockIdx.x * (1 << o.lg) + (threadIdx.x & ((1 << o.lg) - 1));
+  const int64_t rpb = 256 >> o.lg;  // rows per workgroup
   const int64_t c0 = ch * EPC;
   if (ch >= nch) return;
-  for (int64_t r = (int64_t)blockIdx.y * rpb + (threadIdx.x >> lg); r < Rp; r += (int64_t)gridDim.y * rpb) {
+  for (int64_t r = (int64_t)blockIdx.y * rpb + (threadIdx.x >> o.lg); r < o.Rp; r += (int64_t)gridDim.y * rpb) {
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (r < R && c0 < C) {
-      const uintptr_t start = reinterpret_cast<uintptr_t>(in) + (uintptr_t)(r * ld * ESZ);
+    if (r < o.R && c0 < o.C) {
+      const uintptr_t start = reinterpret_cast<uintptr_t>(o.in) + (uintptr_t)(r * o.ld * ESZ);
       const uint32_t b = (uint32_t)(start & 15);  // the row's byte misalignment
       const uintptr_t lo = start - b + (uintptr_t)(c0 * ESZ);
       const u32x4 a0 = *reinterpret_cast<const u32x4*>(lo);
       u32x4 a1 = {0u, 0u, 0u, 0u};
-      if (b != 0 && c0 * ESZ + 16 < (int64_t)b + C * ESZ) a1 = *reinterpret_cast<const u32x4*>(lo + 16);
+      if (b != 0 && c0 * ESZ + 16 < (int64_t)b + o.C * ESZ) a1 = *reinterpret_cast<const u32x4*>(lo + 16);
       v = funnel16(a0, a1, b);
-      if (c0 + EPC > C) v = keep_bytes(v, (int)(C - c0) * ESZ);  // the row's last chunk: zero past C
+      if (c0 + EPC > o.C) v = keep_bytes(v, (int)(o.C - c0) * ESZ);  // the row's last chunk: zero past C
     }
-    *reinterpret_cast<u32x4*>(out + (r * Cp + c0) * ESZ) = v;
+    *reinterpret_cast<u32x4*>(o.out + (r * o.Cp + c0) * ESZ) = v;
   }
 }
 
+// Padding copies of two operands (each: in, out, R, C, ld, Rp, Cp).
 template <int ESZ>
-inline hipError_t pad_copy(const void* in, void* out, int64_t R, int64_t C, int64_t ld, int64_t Rp, int64_t Cp,
+inline hipError_t pad_copy(const void* in0, void* out0, int64_t R0, int64_t C0, int64_t ld0, int64_t Rp0, int64_t Cp0,
+                           const void* in1, void* out1, int64_t R1, int64_t C1, int64_t ld1, int64_t Rp1, int64_t Cp1,
                            hipStream_t stream) {
-  if (Rp == 0 || Cp == 0) return hipSuccess;
-  const int64_t nch = Cp / (16 / ESZ);
-  int lg = 0;
-  while (lg < 8 && (int64_t(1) << lg) < nch) ++lg;
-  const int64_t rpb = 256 >> lg;
-  const dim3 grid((unsigned)((nch + (1 << lg) - 1) >> lg), (unsigned)std::min<int64_t>((Rp + rpb - 1) / rpb, 65535));
-  hipLaunchKernelGGL(pad_copy_kernel<ESZ>, grid, dim3(256), 0, stream, static_cast<const unsigned char*>(in),
-                     static_cast<unsigned char*>(out), R, C, ld, Rp, Cp, lg);
+  int64_t gx = 0, gy = 0;
+  auto op = [&](const void* in, void* out, int64_t R, int64_t C, int64_t ld, int64_t Rp, int64_t Cp) {
+    PadCopyOp o{static_cast<const unsigned char*>(in), static_cast<unsigned char*>(out), R, C, ld, Rp, Cp, 0};
+    const int64_t nch = Cp / (16 / ESZ);
+    while (o.lg < 8 && (int64_t(1) << o.lg) < nch) ++o.lg;
+    const int64_t rpb = 256 >> o.lg;
+    gx = std::max(gx, (nch + (1 << o.lg) - 1) >> o.lg);
+    gy = std::max(gy, std::min<int64_t>((Rp + rpb - 1) / rpb, 65535));
+    return o;
+  };
+  const PadCopyOp o0 = op(in0, out0, R0, C0, ld0, Rp0, Cp0), o1 = op(in1, out1, R1, C1, ld1, Rp1, Cp1);
+  if (gx == 0 || gy == 0) return hipSuccess;
+  hipLaunchKernelGGL(pad_copy_kernel<ESZ>, dim3((unsigned)gx, (unsigned)gy, 2), dim3(256), 0, stream, o0, o1);
   return hipGetLastError();
 }
 

@@ -425,9 +425,7 @@ hipError_t launch_gemm_bf16_pad(const MatmulArgs& a) {
   char* ws = static_cast<char*>(a.workspace);
   u16* x1p = reinterpret_cast<u16*>(ws);
   u16* x2p = reinterpret_cast<u16*>(ws + p.x1_bytes);
-  hipError_t e = pad_copy<2>(a.x1, x1p, r1, c1, a.ldx1, r1p, c1p, a.stream);
-  if (e != hipSuccess) return e;
-  e = pad_copy<2>(a.x2, x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
+  const hipError_t e = pad_copy<2>(a.x1, x1p, r1, c1, a.ldx1, r1p, c1p, a.x2, x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
   if (e != hipSuccess) return e;
   MatmulArgs b = a;
   b.x1 = x1p;

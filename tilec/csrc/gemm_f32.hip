@@ -487,9 +487,7 @@ hipError_t launch_gemm_f32_pad(const MatmulArgs& a) {
   char* ws = static_cast<char*>(a.workspace);
   float* x1p = reinterpret_cast<float*>(ws);
   float* x2p = reinterpret_cast<float*>(ws + p.x1_bytes);
-  hipError_t e = pad_copy<4>(a.x1, x1p, r1, c1, a.ldx1, r1p, c1p, a.stream);
-  if (e != hipSuccess) return e;
-  e = pad_copy<4>(a.x2, x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
+  const hipError_t e = pad_copy<4>(a.x1, x1p, r1, c1, a.ldx1, r1p, c1p, a.x2, x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
   if (e != hipSuccess) return e;
   MatmulArgs b = a;
   b.x1 = x1p;
