@@ -623,17 +623,20 @@ hipError_t launch_skinny(const MatmulArgs& a) {
 // AL: every row starts on a 16-byte boundary (K, both strides and both
 // bases aligned).  Otherwise (any element alignment) each row's resource
 // starts at the 16-byte boundary below the row and ends at the one above
-// its last element, a lane loads the two aligned chunks its 16 bytes span
-// and shifts them into place by the row's byte misalignment (funnel16), and
-// elements past K, which now share a chunk with the next row, are cleared
-// in both operands.  No load leaves the row's own 16-byte chunks.
+// its last element, and a wave load covers 63 lanes' worth of the row
+// (chunks 1008 bytes apart, overlapping by 16): lane l < 63 loads the
+// aligned 16 bytes at 16 l, takes lane l + 1's with a lane shuffle, and
+// shifts the pair into place by the row's byte misalignment (funnel16);
+// lane 63 only supplies its load.  Elements past K, which now share a chunk
+// with the next row, are cleared in both operands.  No load leaves the
+// row's own 16-byte chunks.
 // ---------------------------------------------------------------------------
 template <typename T, int MR, int RPW, int WAVES, int U, int CP, bool AL>
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restrict__ x1, const T* __restrict__ w,
                                                                float* __restrict__ out, int M, int N, int K,
                                                                int64_t ldx1, int64_t ldw, int64_t ldo) {
   constexpr int EPL = 16 / (int)sizeof(T);  // elements per 16-byte load
-  constexpr int CH = 64 * EPL;             // K elements per wave load
+  constexpr int CH = (AL ? 64 : 63) * EPL;  // K elements per wave load
   typedef std::conditional_t<sizeof(T) == 4, f32x4, i32x4> V;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -666,9 +669,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
     if constexpr (sizeof(T) == 4) return v[e];
     else return (e & 1) ? bf16_hi(v[e >> 1]) : bf16_lo(v[e >> 1]);
   };
-  constexpr int NH = AL ? 1 : 2;  // aligned chunks loaded per 16 bytes used
   struct Batch {
-    V w[U][RPW][NH], x[U][MR][NH];
+    V w[U][RPW], x[U][MR];
   };
   float acc[RPW][MR];
 #pragma unroll
@@ -682,20 +684,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
       // chunk c0 + u; past K every element is masked (offset >= extent)
       const uint32_t off = (uint32_t)(c0 + u) * (uint32_t)CH * sizeof(T) + lane_off;
 #pragma unroll
-      for (int h = 0; h < NH; ++h) {
+      for (int r = 0; r < RPW; ++r) b.w[u][r] = ld_w(rw[r], off);
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) b.w[u][r][h] = ld_w(rw[r], off + 16u * h);
-#pragma unroll
-        for (int m = 0; m < MR; ++m) b.x[u][m][h] = ld(rx[m], off + 16u * h);
-      }
+      for (int m = 0; m < MR; ++m) b.x[u][m] = ld(rx[m], off);
     }
   };
   // The 16 bytes a lane uses (AL: as loaded).
-  auto use = [&](const V (&v)[NH], uint32_t b, int kvalid) -> V {
+  auto use = [&](const V& v, uint32_t b, int kvalid) -> V {
     if constexpr (AL) {
-      return v[0];
+      return v;
     } else {
-      u32x4 x = funnel16(__builtin_bit_cast(u32x4, v[0]), __builtin_bit_cast(u32x4, v[NH - 1]), b);
+      const u32x4 lo = __builtin_bit_cast(u32x4, v);
+      u32x4 hi;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hi[j] = (uint32_t)__shfl_down((int)lo[j], 1);
+      u32x4 x = funnel16(lo, hi, b);
       if (kvalid < EPL) x = keep_bytes(x, kvalid * (int)sizeof(T));
       return __builtin_bit_cast(V, x);
     }
@@ -703,7 +706,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
   auto fma = [&](int c0, const Batch& b) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int kvalid = K - (c0 + u) * CH - EPL * lane;  // elements of this lane's 16 bytes inside K
+      // elements of this lane's 16 bytes inside K (the unaligned form's lane
+      // 63 has none of its own)
+      const int kvalid = (!AL && lane == 63) ? 0 : K - (c0 + u) * CH - EPL * lane;
       V wv[RPW], xv[MR];
 #pragma unroll
       for (int r = 0; r < RPW; ++r) wv[r] = use(b.w[u][r], bw[r], kvalid);
