@@ -416,26 +416,33 @@ __device__ __forceinline__ u32x4 keep_bytes(u32x4 v, int keep) {
 }
 
 // One operand of a padding copy: in (R x C, row stride ld) -> out (Rp x Cp,
-// row stride Cp); rows of 2^lg threads.
+// row stride Cp); rows of 2^lg threads, a gx x gy grid of workgroups.
 struct PadCopyOp {
   const unsigned char* in;
   unsigned char* out;
   int64_t R, C, ld, Rp, Cp;
-  int lg;
+  int lg, gx, gy;
 };
 
-// Both operands in one launch (grid z selects the operand): at the sizes
-// where the pad variants win, a second launch's fixed cost is a few per cent.
+// Both operands in one launch: workgroups 0 .. gx0 gy0 - 1 copy the first,
+// the rest the second (each operand its own grid, so one with few rows or
+// narrow rows launches no empty workgroups for the other's shape).  At the
+// sizes where the pad variants win, a second launch's fixed cost is a few
+// per cent.
 template <int ESZ>
 __global__ __launch_bounds__(256) void pad_copy_kernel(PadCopyOp o0, PadCopyOp o1) {
   constexpr int EPC = 16 / ESZ;  // elements per 16-byte chunk
-  const PadCopyOp& o = blockIdx.z ? o1 : o0;
+  const int n0 = o0.gx * o0.gy;
+  const bool second = (int)blockIdx.x >= n0;
+  const PadCopyOp& o = second ? o1 : o0;
+  const int blk = (int)blockIdx.x - (second ? n0 : 0);
+  const int bx = blk % o.gx, by = blk / o.gx;
   const int64_t nch = o.Cp / EPC;
-  const int64_t ch = (int64_t)blockIdx.x * (1 << o.lg) + (threadIdx.x & ((1 << o.lg) - 1));
+  const int64_t ch = (int64_t)bx * (1 << o.lg) + (threadIdx.x & ((1 << o.lg) - 1));
   const int64_t rpb = 256 >> o.lg;  // rows per workgroup
   const int64_t c0 = ch * EPC;
   if (ch >= nch) return;
-  for (int64_t r = (int64_t)blockIdx.y * rpb + (threadIdx.x >> o.lg); r < o.Rp; r += (int64_t)gridDim.y * rpb) {
+  for (int64_t r = (int64_t)by * rpb + (threadIdx.x >> o.lg); r < o.Rp; r += (int64_t)o.gy * rpb) {
     u32x4 v = {0u, 0u, 0u, 0u};
     if (r < o.R && c0 < o.C) {
       const uintptr_t start = reinterpret_cast<uintptr_t>(o.in) + (uintptr_t)(r * o.ld * ESZ);
@@ -456,19 +463,23 @@ template <int ESZ>
 inline hipError_t pad_copy(const void* in0, void* out0, int64_t R0, int64_t C0, int64_t ld0, int64_t Rp0, int64_t Cp0,
                            const void* in1, void* out1, int64_t R1, int64_t C1, int64_t ld1, int64_t Rp1, int64_t Cp1,
                            hipStream_t stream) {
-  int64_t gx = 0, gy = 0;
-  auto op = [&](const void* in, void* out, int64_t R, int64_t C, int64_t ld, int64_t Rp, int64_t Cp) {
-    PadCopyOp o{static_cast<const unsigned char*>(in), static_cast<unsigned char*>(out), R, C, ld, Rp, Cp, 0};
+  auto op = [](const void* in, void* out, int64_t R, int64_t C, int64_t ld, int64_t Rp, int64_t Cp) {
+    PadCopyOp o{static_cast<const unsigned char*>(in), static_cast<unsigned char*>(out), R, C, ld, Rp, Cp, 0, 0, 0};
     const int64_t nch = Cp / (16 / ESZ);
     while (o.lg < 8 && (int64_t(1) << o.lg) < nch) ++o.lg;
     const int64_t rpb = 256 >> o.lg;
-    gx = std::max(gx, (nch + (1 << o.lg) - 1) >> o.lg);
-    gy = std::max(gy, std::min<int64_t>((Rp + rpb - 1) / rpb, 65535));
+    const int64_t gx = (nch + (1 << o.lg) - 1) >> o.lg;
+    int64_t gy = Rp > 0 && gx > 0 ? (Rp + rpb - 1) / rpb : 0;
+    while (gy > 1 && gx * gy > (int64_t(1) << 29)) gy = (gy + 1) / 2;  // the row loop strides over the rest
+    o.gx = (int)gx;
+    o.gy = (int)gy;
     return o;
   };
   const PadCopyOp o0 = op(in0, out0, R0, C0, ld0, Rp0, Cp0), o1 = op(in1, out1, R1, C1, ld1, Rp1, Cp1);
-  if (gx == 0 || gy == 0) return hipSuccess;
-  hipLaunchKernelGGL(pad_copy_kernel<ESZ>, dim3((unsigned)gx, (unsigned)gy, 2), dim3(256), 0, stream, o0, o1);
+  const int64_t blocks = (int64_t)o0.gx * o0.gy + (int64_t)o1.gx * o1.gy;
+  if (blocks == 0) return hipSuccess;
+  if ((int64_t)o0.gx * o0.gy >= (int64_t(1) << 30) || blocks >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pad_copy_kernel<ESZ>, dim3((unsigned)blocks), dim3(256), 0, stream, o0, o1);
   return hipGetLastError();
 }
 
