@@ -212,6 +212,10 @@ def test_tune_features_and_shapes():
     assert fb(1024, 4096, 1024, 256, "bf16", "gemm_bf16_128x128x64_r4_kc", 1, 3) == 0.0
     assert fb(1020, 4096, 1024, 256, "bf16", "gemm_bf16_64x64x64_w2x2", 1, 1) == 0.0
     assert fb(16, 4097, 4096, 256, "f32", "skinny_f32_w8_b1", 1, 0) == 0.0
+    # the row-dot kernel's shifted form for K past whole 16-byte groups; the row-tile kernel never runs there
+    assert fb(4, 5429, 11110, 256, "bf16", "skinny_bf16_t4_r2_w4", 1, 2) == 1.0
+    assert fb(4, 5432, 11110, 256, "bf16", "skinny_bf16_t4_r2_w4", 1, 2) == 0.0
+    assert fb(4, 5432, 11110, 256, "bf16", "skinny_bf16_t16_r16_w8_c128", 1, 2) == 0.0
     # copies before the GEMM enter the analytic time: a launch each and their bytes
     assert tune.prepass(1000, 4097, 3001, "f32", "gemm_f32_64x64x32_w2x2_pad") == (2, 8 * (1000 * 4097 + 4097 * 3001))
     assert tune.prepass(1024, 512, 640, "bf16", "gemm_bf16_128x128x64_r4_kc", 1) == (2, 4 * (1024 * 512 + 512 * 640))

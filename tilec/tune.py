@@ -26,6 +26,7 @@ import json
 import math
 import os
 import random
+import re
 import sys
 from functools import lru_cache
 
@@ -145,14 +146,19 @@ def features(M, K, N, cus, dtype, kernel, split_k, layout=0):
 
 
 def falls_back(kernel, M, K, N, dtype, layout=0):
-    """Whether a tile-GEMM variant runs a slower fallback of its tile for
-    these operands: the direct-to-LDS tiles (fp32 `*_lds`, the bf16 tiles
-    with a ring of stage buffers) take only operands whose contiguous extents
-    are whole 16-byte groups.  The bf16 transposing variants (`*_kc`) copy
-    operands whose M, N and K are multiples of 8 into that form and run the
-    plain tile on the others.  The pad variants exist for the other shapes
-    and never fall back."""
+    """Whether a variant runs a slower form of its kernel for these operands:
+    the direct-to-LDS tiles (fp32 `*_lds`, the bf16 tiles with a ring of
+    stage buffers) take only operands whose contiguous extents are whole
+    16-byte groups and run a register-staged fallback otherwise.  The bf16
+    transposing variants (`*_kc`) copy operands whose M, N and K are
+    multiples of 8 into that form and run the plain tile on the others.  The
+    row-dot kernel (`x @ W.T`, M <= 4) shifts every 16-byte piece into place
+    when K is not a whole number of 16-byte groups.  The pad variants exist
+    for the other shapes and never fall back."""
     v = _variant_by_name()[kernel]
+    if v["family"] == _lib.FAMILY_SKINNY and re.search(r"_t\d+_r\d+_", kernel) and not kernel.endswith(
+            ("_c128", "_c256")):
+        return not aligned(K, dtype)
     if v["family"] != _lib.FAMILY_GEMM or kernel.endswith("_pad"):
         return False
     if kernel.endswith("_kc") and M % 8 == 0 and N % 8 == 0 and K % 8 == 0:
