@@ -683,12 +683,15 @@ def _view_at(x, col, off, extra):
 
 def test_pad_variants_any_alignment():
     """The pad variants (operands copied into the workspace with 16-byte rows,
-    every row's bytes shifted into place) on operands at every element
+    every row's bytes shifted into place; with K a whole number of K steps an
+    aligned operand is read in place) on operands at every element
     misalignment of base and row stride, in every layout, K splits where the
     tile splits: the fp64 oracle, and small integers exactly."""
     pads = [v for v in _lib.variants() if v["name"].endswith("_pad")]
     assert len(pads) == 5
-    shapes = [(67, 1001, 93), (130, 515, 264), (5, 77, 9), (300, 200, 131)]
+    # K a whole number of K steps (64 and 32 divide 512 and 1024): operands
+    # whose rows are already whole 16-byte groups are read in place
+    shapes = [(67, 1001, 93), (130, 515, 264), (5, 77, 9), (300, 200, 131), (130, 512, 261), (67, 1024, 96)]
     for i, (m, k, n) in enumerate(shapes):
         a, b = O.normal((m, k), 1400 + 2 * i), O.normal((k, n), 1401 + 2 * i)
         ai, bi = O.small_ints((m, k), 1420 + 2 * i, -3, 3), O.small_ints((k, n), 1421 + 2 * i, -3, 3)

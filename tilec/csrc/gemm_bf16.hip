@@ -368,9 +368,11 @@ hipError_t launch_gemm_bf16_kc(const MatmulArgs& a) {
 // contiguous extent or row stride not a multiple of 8 elements, e.g. an odd
 // K) cannot take the LDS-DMA kernel's 16-byte copies, and the plain variants
 // run the generic kernel for it (2-3x slower on MI355X).  These variants
-// first copy both operands into the workspace in the caller's layout, the
+// first copy the operands into the workspace in the caller's layout, the
 // contiguous extent and row stride rounded up to 8 elements and K up to the
-// K step, zero-filled, then run the LDS-DMA kernel on the copies.  Zeros add
+// K step, zero-filled (both operands when K is not a whole number of K
+// steps, else only those whose rows are not whole 16-byte groups), then run
+// the LDS-DMA kernel.  Zeros add
 // nothing to the product; C is written as the caller's M x N (column chunks
 // past N may read padding, never store it).  Workspace: [x1 padded][x2
 // padded][split-K partials], each 256-byte aligned.  The copies are
@@ -422,17 +424,26 @@ hipError_t launch_gemm_bf16_pad(const MatmulArgs& a) {
   if ((ca ? BK : BM) * c1p * 2 >= lim || (cb ? BN : BK) * c2p * 2 >= lim || std::max(r1p, c1p) >= lim ||
       std::max(r2p, c2p) >= lim || reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0)
     return launch_gemm_bf16<BM, BN, BK, NBUF, WM, WN, MF>(a);
+  // With K a whole number of K steps, an operand whose rows are already whole
+  // 16-byte groups (extent, stride and base) is read in place; only the
+  // other is copied.
+  auto in_place = [&](const void* x, int64_t c, int64_t ld, int64_t rows_per_step) {
+    return a.K % BK == 0 && c % 8 == 0 && ld % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           rows_per_step * ld * 2 < lim;
+  };
+  const bool keep1 = in_place(a.x1, c1, a.ldx1, ca ? BK : BM), keep2 = in_place(a.x2, c2, a.ldx2, cb ? BN : BK);
   char* ws = static_cast<char*>(a.workspace);
   u16* x1p = reinterpret_cast<u16*>(ws);
   u16* x2p = reinterpret_cast<u16*>(ws + p.x1_bytes);
-  const hipError_t e = pad_copy<2>(a.x1, x1p, r1, c1, a.ldx1, r1p, c1p, a.x2, x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
+  const hipError_t e = pad_copy<2>(a.x1, x1p, r1, c1, a.ldx1, keep1 ? 0 : r1p, c1p, a.x2, x2p, r2, c2, a.ldx2,
+                                   keep2 ? 0 : r2p, c2p, a.stream);
   if (e != hipSuccess) return e;
   MatmulArgs b = a;
-  b.x1 = x1p;
-  b.x2 = x2p;
+  b.x1 = keep1 ? a.x1 : x1p;
+  b.x2 = keep2 ? a.x2 : x2p;
   b.K = p.kp;
-  b.ldx1 = c1p;
-  b.ldx2 = c2p;
+  b.ldx1 = keep1 ? a.ldx1 : c1p;
+  b.ldx2 = keep2 ? a.ldx2 : c2p;
   b.workspace = ws + p.x1_bytes + p.x2_bytes;
   b.workspace_bytes = a.workspace_bytes - p.x1_bytes - p.x2_bytes;
   switch (a.layout & 3) {

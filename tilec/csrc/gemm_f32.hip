@@ -484,17 +484,26 @@ hipError_t launch_gemm_f32_pad(const MatmulArgs& a) {
   if ((ca ? BK : BM) * c1p * 4 >= lim || (cb ? BN : BK) * c2p * 4 >= lim || r1p * c1p >= (int64_t(1) << 31) ||
       r2p * c2p >= (int64_t(1) << 31) || reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0)
     return launch_gemm_f32<BM, BN, BK, WM, WN>(a);
+  // With K a whole number of K steps, an operand whose rows are already whole
+  // 16-byte groups (extent, stride and base) is read in place; only the
+  // other is copied.
+  auto in_place = [&](const void* x, int64_t c, int64_t ld, int64_t rows_per_step) {
+    return a.K % BK == 0 && c % 4 == 0 && ld % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           rows_per_step * ld * 4 < lim;
+  };
+  const bool keep1 = in_place(a.x1, c1, a.ldx1, ca ? BK : BM), keep2 = in_place(a.x2, c2, a.ldx2, cb ? BN : BK);
   char* ws = static_cast<char*>(a.workspace);
   float* x1p = reinterpret_cast<float*>(ws);
   float* x2p = reinterpret_cast<float*>(ws + p.x1_bytes);
-  const hipError_t e = pad_copy<4>(a.x1, x1p, r1, c1, a.ldx1, r1p, c1p, a.x2, x2p, r2, c2, a.ldx2, r2p, c2p, a.stream);
+  const hipError_t e = pad_copy<4>(a.x1, x1p, r1, c1, a.ldx1, keep1 ? 0 : r1p, c1p, a.x2, x2p, r2, c2, a.ldx2,
+                                   keep2 ? 0 : r2p, c2p, a.stream);
   if (e != hipSuccess) return e;
   MatmulArgs b = a;
-  b.x1 = x1p;
-  b.x2 = x2p;
+  b.x1 = keep1 ? a.x1 : x1p;
+  b.x2 = keep2 ? a.x2 : x2p;
   b.K = p.kp;
-  b.ldx1 = c1p;
-  b.ldx2 = c2p;
+  b.ldx1 = keep1 ? a.ldx1 : c1p;
+  b.ldx2 = keep2 ? a.ldx2 : c2p;
   b.workspace = ws + p.x1_bytes + p.x2_bytes;
   b.workspace_bytes = a.workspace_bytes - p.x1_bytes - p.x2_bytes;
   switch (a.layout & 3) {
