@@ -84,6 +84,11 @@ def test_hip_configs_rules():
     assert not ext.direct_regime(2049, 2048, "f32") and not ext.direct_regime(1024, 1024, "bf16")
     assert any(c[0].startswith("direct_") for c in ext.hip_configs(1024, 1024, 1024, "f32"))
     assert not any(c[0].startswith("direct_") for c in ext.hip_configs(4096, 4096, 4096, "f32"))
+    # 2048 x 2048 x 16384: 1024 64x64 tiles (2048 of 32x64): at 256 CUs the 8-per-CU cap leaves the
+    # direct kernel a K split of 2 at most, where a split of 64 would launch 131 072 workgroups
+    big = [c for c in ext.hip_configs(2048, 16384, 2048, "f32") if c[0].startswith("direct_")]
+    if ext.device_cus() == 256:
+        assert big and max(ext._direct_splits(16384, s) for _, s in big) == 2
     # no direct config past the library's 2 GiB partials limit is offered
     names = {v["name"]: v for v in _lib.variants()}
     for M, K, N in [(2048, 4096, 2048), (1024, 1024, 1024), (513, 3001, 127), (1, 65536, 4096)]:
@@ -107,6 +112,9 @@ def test_hip_configs_rules():
                 assert dt == "f32" and v["bm"] < 2 * max(M, 16)
                 assert ext.skinny_regime(M, N, dt) or ext.direct_regime(M, N, dt)
                 assert eff == 1 or ext.cdiv(K, eff) >= 16 * v["waves"]
+                # a K split keeps the grid within 8 workgroups per CU
+                tiles = ext.cdiv(M, v["bm"]) * ext.cdiv(N, v["bn"])
+                assert eff == 1 or tiles * eff <= 8 * ext.device_cus()
             else:
                 tiles = ext.cdiv(M, v["bm"]) * ext.cdiv(N, v["bn"])
                 eff = ext._gemm_splits(K, s, v["bk"])

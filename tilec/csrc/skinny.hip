@@ -771,26 +771,39 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const T* __restri
 // apart: the 16-byte skew makes the operand reads below conflict-free), and
 // reads them back as MFMA operands: for each 64-byte k group t of the chunk,
 // lane l reads 16 bytes of row l % 16 at byte 64 t + 16 (l / 16).  The
-// matching x1 pieces, x1[l % 16][same k], come straight from the cache as the
-// B operand, so D[i][j] accumulates out[j][n0 + i]:
+// matching x1 pieces, x1[l % 16][same k], are the B operand, so D[i][j]
+// accumulates out[j][n0 + i]:
 //   fp32: the 16 bytes are k = 4 g + u (g = l / 16, u < 4), one
 //         v_mfma_f32_16x16x4f32 per u;
 //   bf16: the 16 bytes are 8 consecutive k, one v_mfma_f32_16x16x32_bf16.
 // Which k meets which MFMA slot does not matter to the sum as long as A and B
 // agree, and they do (same byte offsets in W's row and x1's row).
 //
-// Only a wave's own LDS area is written and read in the loop (LDS runs a
+// x1 takes the same route as W: loaded as whole CHB-byte row pieces (8 or 4
+// rows of 128 or 256 bytes per wave load), staged in a second LDS area and
+// read back in the operand layout.  Read directly in that layout, each load
+// of x1 would touch 16 rows at 64 bytes each — twice the cache lines per
+// byte of a W load — and every workgroup reads all of x1 from the L2 (as
+// many bytes as it reads of W at M = 16).  And workgroup b of G starts its
+// sweep over K nch * b / G chunks in (wrapping around): in lockstep, all
+// workgroups would read the same K columns of x1 at once, 16 rows at a
+// stride of ldx1, which lands on a few L2 channels.  On MI355X at
+// K = N = 4096 the two took fp32 M = 16 from 15.3-18.2 us to 14.0 us.
+//
+// Only a wave's own LDS areas are written and read in the loop (LDS runs a
 // wave's operations in order), so the loop has no barrier.  Masking is on
 // addresses: W rows past N, x1 rows past M and k past K load zeros (both
-// operands, so NaN padding past K cannot leak in).  Rows of the LDS area past
+// operands, so NaN padding past K cannot leak in).  Rows of the W area past
 // R are never written; they only feed D rows that are not stored.  A ring of
 // NB register sets keeps the loads of NB - 1 chunks in flight while a chunk
-// is multiplied.  Small chunks (128 or 256 bytes per row: 8 or 4 rows of W
-// per wave load) and many waves keep each wave's MFMA work per chunk short,
-// so the last chunks to arrive are multiplied quickly; 512-byte and 1 KiB
-// chunks left fp32 launches waiting on MFMAs after their data had arrived.
+// is multiplied; one or two sets did best (fp32 M = 16: 13.0 us with two,
+// 14.0 with four, 15.3 with eight — deeper rings queue more requests behind
+// each other without reading faster).  Small chunks (128 or 256 bytes per
+// row) and many waves keep each wave's MFMA work per chunk short, so the
+// last chunks to arrive are multiplied quickly; 512-byte and 1 KiB chunks
+// left fp32 launches waiting on MFMAs after their data had arrived.
 // Summing the waves in a fixed order keeps results independent of
-// scheduling.
+// scheduling; the rotation fixes each workgroup's order of chunks too.
 // ---------------------------------------------------------------------------
 template <typename T, int WAVES, int CHB, int R, int NB>
 __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict__ x1, const T* __restrict__ w,
@@ -804,7 +817,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
   static_assert(CHB == 128 || CHB == 256 || CHB == 512 || CHB == 1024, "chunk of 128 to 1024 bytes per row");
   static_assert(R <= 16 && R % RPI == 0, "R rows of W, whole wave loads");
   typedef std::conditional_t<sizeof(T) == 4, f32x4, i32x4> V;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[WAVES * 16 * PITCH];
+  constexpr int AREA = 2 * 16 * PITCH;  // the wave's W rows, then its x1 rows
+  __shared__ __attribute__((aligned(16))) unsigned char lds[WAVES * AREA];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -817,9 +831,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
   const BufRsrc rx = make_rsrc(x1 + (int64_t)m0 * ldx1);
   const int wrow = lane / LPR;                     // row of a wave load this lane reads
   const uint32_t wcol = 16u * (uint32_t)(lane % LPR);  // its byte within the row piece
-  const bool xrow = m0 + q < M;
-  const uint32_t xoff = (uint32_t)q * ldx1_b + 16u * (uint32_t)g;
-  unsigned char* const area = lds + wave * 16 * PITCH;
+  unsigned char* const area = lds + wave * AREA;
+  unsigned char* const xarea = area + 16 * PITCH;
 
   struct Batch {
     V w[NLD], x[KG];
@@ -827,11 +840,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
   // x1 pieces of chunk c: lane l reads x1[m0 + l % 16][k group t, 16 bytes at 16 (l / 16)]
   auto load_x = [&](int c, V* x) __attribute__((always_inline)) {
     const uint32_t cb = (uint32_t)c * CHB;
+    const bool kw = cb + wcol < kbytes;
 #pragma unroll
-    for (int t = 0; t < KG; ++t) {
-      const uint32_t kb = cb + 64u * t + 16u * g;
-      const bool ok = xrow && kb < kbytes;
-      x[t] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(ok ? xoff + cb + 64u * t : kOob), 0, 0));
+    for (int i = 0; i < KG; ++i) {
+      const int r = i * RPI + wrow;
+      const bool ok = kw && m0 + r < M;
+      x[i] = __builtin_bit_cast(
+          V, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(ok ? (uint32_t)r * ldx1_b + cb + wcol : kOob), 0, 0));
     }
   };
   auto load = [&](int c, Batch& b) __attribute__((always_inline)) {
@@ -852,27 +867,38 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
     for (int i = 0; i < NLD; ++i)
       *reinterpret_cast<V*>(area + (i * RPI + wrow) * PITCH + wcol) = b.w[i];
 #pragma unroll
+    for (int i = 0; i < KG; ++i)
+      *reinterpret_cast<V*>(xarea + (i * RPI + wrow) * PITCH + wcol) = b.x[i];
+#pragma unroll
     for (int t = 0; t < KG; ++t) {
       const V a = *reinterpret_cast<const V*>(area + q * PITCH + 64 * t + 16 * g);
+      const V xb = *reinterpret_cast<const V*>(xarea + q * PITCH + 64 * t + 16 * g);
       if constexpr (sizeof(T) == 4) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t & 1] = mfma16x16x4(a[u], b.x[t][u], acc[t & 1]);
+        for (int u = 0; u < 4; ++u) acc[t & 1] = mfma16x16x4(a[u], xb[u], acc[t & 1]);
       } else {
-        acc[t & 1] = mfma16x16x32bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b.x[t]), acc[t & 1]);
+        acc[t & 1] = mfma16x16x32bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, xb), acc[t & 1]);
       }
     }
   };
   const int nch = (int)((kbytes + CHB - 1) / CHB);
   const int mine = nch > wave ? (nch - wave + WAVES - 1) / WAVES : 0;  // chunks wave, wave + WAVES, ...
+  // Workgroup b starts its sweep nch * b / G chunks into K (G workgroups)
+  // and wraps around; chunk numbers past nch stay past it (masked loads).
+  const int rot = (int)(((int64_t)blockIdx.x * nch) / (int)gridDim.x);
+  auto chunk = [&](int c) {
+    const int r = c + rot;
+    return c < nch ? (r >= nch ? r - nch : r) : c;
+  };
   // Ring of NB register sets: chunk j + NB - 1 is loaded before chunk j is
   // used (loads past the last chunk are masked and touch no memory).
   Batch ring[NB];
 #pragma unroll
-  for (int s = 0; s < NB - 1; ++s) load(wave + s * WAVES, ring[s]);
+  for (int s = 0; s < NB - 1; ++s) load(chunk(wave + s * WAVES), ring[s]);
   for (int j = 0; j < mine; j += NB) {
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
-      load(wave + (j + s + NB - 1) * WAVES, ring[(s + NB - 1) % NB]);
+      load(chunk(wave + (j + s + NB - 1) * WAVES), ring[(s + NB - 1) % NB]);
       __builtin_amdgcn_sched_barrier(0);
       if (j + s < mine) mma(ring[s]);
       __builtin_amdgcn_sched_barrier(0);
@@ -885,7 +911,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wt_kernel(const T* __restrict
   if (wave != 0) return;
   f32x4 s = *reinterpret_cast<const f32x4*>(lds + 16 * lane);
 #pragma unroll
-  for (int v = 1; v < WAVES; ++v) s += *reinterpret_cast<const f32x4*>(lds + v * 16 * PITCH + 16 * lane);
+  for (int v = 1; v < WAVES; ++v) s += *reinterpret_cast<const f32x4*>(lds + v * AREA + 16 * lane);
   if (m0 + q >= M) return;
   float* orow = out + (int64_t)(m0 + q) * ldo;
 #pragma unroll
@@ -1007,13 +1033,13 @@ const VariantDesc* skinny_variants(int* count) {
       rows_desc({"skinny_f32_t1_r1_w8_u2", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 8, kKcMax, 8, 1, 2, launch_rows_or_skinny<float, 1, 1, 8, 2>}, rows_fit<float, 1>),
       rows_desc({"skinny_bf16_t1_r1_w8_u2", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 8, kKcMax, 8, 1, 2, launch_rows_or_skinny<u16, 1, 1, 8, 2>}, rows_fit<u16, 1>),
       // x @ W.T, M <= 16: row-tile kernel, 16 rows of W per workgroup over all of K (BN), K chunks of
-      // 128 or 256 bytes per row, a ring of 4 register sets; other layouts run skinny_*_w4_b2.
-      rows_desc({"skinny_f32_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<float, 16, 128, 16, 4>}, wt_fits<float, 128, 16>),
-      rows_desc({"skinny_f32_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<float, 8, 128, 16, 4>}, wt_fits<float, 128, 16>),
-      rows_desc({"skinny_f32_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<float, 8, 256, 16, 4>}, wt_fits<float, 256, 16>),
-      rows_desc({"skinny_bf16_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 16, 16, 4, launch_wt_or_skinny<u16, 16, 128, 16, 4>}, wt_fits<u16, 128, 16>),
-      rows_desc({"skinny_bf16_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<u16, 8, 128, 16, 4>}, wt_fits<u16, 128, 16>),
-      rows_desc({"skinny_bf16_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 4, launch_wt_or_skinny<u16, 8, 256, 16, 4>}, wt_fits<u16, 256, 16>),
+      // 128 or 256 bytes per row, a ring of `unroll` register sets; other layouts run skinny_*_w4_b2.
+      rows_desc({"skinny_f32_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 16, 16, 1, launch_wt_or_skinny<float, 16, 128, 16, 1>}, wt_fits<float, 128, 16>),
+      rows_desc({"skinny_f32_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 2, launch_wt_or_skinny<float, 8, 128, 16, 2>}, wt_fits<float, 128, 16>),
+      rows_desc({"skinny_f32_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_F32, kMaxM, 16, kKcMax, 8, 16, 1, launch_wt_or_skinny<float, 8, 256, 16, 1>}, wt_fits<float, 256, 16>),
+      rows_desc({"skinny_bf16_t16_r16_w16_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 16, 16, 1, launch_wt_or_skinny<u16, 16, 128, 16, 1>}, wt_fits<u16, 128, 16>),
+      rows_desc({"skinny_bf16_t16_r16_w8_c128", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 2, launch_wt_or_skinny<u16, 8, 128, 16, 2>}, wt_fits<u16, 128, 16>),
+      rows_desc({"skinny_bf16_t16_r16_w8_c256", TILEC_FAMILY_SKINNY, TILEC_BF16, kMaxM, 16, kKcMax, 8, 16, 1, launch_wt_or_skinny<u16, 8, 256, 16, 1>}, wt_fits<u16, 256, 16>),
   };
   *count = (int)(sizeof(t) / sizeof(t[0]));
   return t;

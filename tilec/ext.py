@@ -89,7 +89,8 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
     MFMAs on operands loaded straight into registers, a K split) are offered
     for M <= 16 and, for fp32, outputs too small to fill the chip with 64x64
     tiles; the direct family also for fp32 outputs of up to four such tiles
-    per CU (direct_regime); the tile GEMMs
+    per CU (direct_regime), with K splits that keep its grid within 8
+    workgroups per CU; the tile GEMMs
     take any M, and K splits too when their own tiles cannot fill the CUs
     (for tiles small enough to split, at least 4 K steps per split).  This
     is the search space of tune.bench / tune.pick, as `mm_configs` is for
@@ -117,8 +118,12 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             if not (skinny_regime(M, N, code) or direct_regime(M, N, code)) or v["bm"] >= 2 * max(M, 16):
                 continue
             # Splits that fill the CUs exactly once or twice over are
-            # offered beside the powers of two; none whose partials would
-            # reach the library's 2 GiB limit.
+            # offered beside the powers of two; none that takes the grid
+            # past 8 workgroups per CU (a K split is there to fill the chip:
+            # on MI355X the cap moved the measured best of 5 of 842 timed
+            # shapes, by at most 3.5 %, and keeps the tuner off splits that
+            # launch 100 000 workgroups) and none whose partials would reach
+            # the library's 2 GiB limit.
             tiles = cdiv(M, v["bm"]) * cdiv(N, v["bn"])
             if tiles == 0:
                 continue  # an empty output: nothing for a K split to fill
@@ -127,6 +132,8 @@ def hip_configs(M, K, N, dtype="f32", layout=None):
             for s in sorted(set(_SKINNY_SPLITS) | set(fills)):
                 eff = _direct_splits(K, s)
                 if eff in seen or (eff > 1 and cdiv(K, eff) < 16 * v["waves"]):
+                    continue
+                if eff > 1 and tiles * eff > 8 * device_cus():
                     continue
                 if eff > 1 and direct_workspace_bytes(v, M, N, eff) >= 1 << 31:
                     continue
